@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Benchmark of the tb.matmul gfx950 path (one MI355X).
+
+Headline (BASELINE.json `metric`): TFLOP/s and fraction of dense FP16 MFMA
+peak on the 4096^3 f16 GEMM (`configs[2]`, the roofline config); a "step" is
+one GEMM launch over inputs already resident in HBM. The same JSON line also
+carries microseconds per launch for the small shapes and the split-K and
+persistent workloads (`extra`), the live roofline of the dominant kernel and
+the host fp32 CPU baseline (the oracle's blocked OpenMP GEMM on this box's
+cores, on a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
+       [--no-cpu] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS_F16 = 2500.0  # MI355X dense FP16 MFMA (published, no sparsity)
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_workload(w, steps: int, warmup: int, device):
+    """Launch `w` steps times; wall clock over the timed region plus per-launch
+    HIP event durations recorded on the launch stream."""
+    import torch
+    import mini_triton_nvgpu_v1_amd as tb
+
+    desc = tb.GemmDesc.from_config(w.direct_config())
+    A = torch.empty((w.M, w.K), dtype=torch.float16, device=device)
+    B = torch.empty((w.K, w.N), dtype=torch.float16, device=device)
+    C = torch.empty((w.M, w.N), dtype=torch.float16, device=device)
+    ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=device)
+          if desc.workspace_bytes else None)
+    stream = torch.cuda.current_stream(device)
+    tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
+    tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
+    for _ in range(warmup):
+        desc.launch(A, B, C, ws, stream=stream)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize(device)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        desc.launch(A, B, C, ws, stream=stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    durs_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    finite = bool(torch.isfinite(C).all().item())
+    return {"wall_s": wall, "kernel_ms": durs_ms, "kernel": desc.kernel_name,
+            "finite": finite}
+
+
+def cpu_baseline(w, budget_s: float = 12.0):
+    """Host fp32 GEMM (oracle/oracle.c tbo_gemm_f32) on the same seeded inputs.
+
+    Sample: the full M x N x K product of the workload when one repetition
+    fits the budget, else a slab of rows; repeated until `budget_s` elapses."""
+    import numpy as np
+    import oracle
+
+    threads = oracle.max_threads()
+    rows = w.M
+    A16, B16 = oracle.config_inputs(rows, w.N, w.K, w.seed, w.dist)
+    A = A16.astype(np.float32)
+    B = B16.astype(np.float32)
+    flop = 2.0 * rows * w.N * w.K
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        oracle.gemm_f32(A, B, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    best = min(times)
+    med = statistics.median(times)
+    return {"value": flop / med / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"{len(times)} x fp32 {rows}x{w.N}x{w.K} GEMM on host "
+                       f"(oracle tbo_gemm_f32, OpenMP {threads} threads, median "
+                       f"{med * 1e3:.1f} ms, best {best * 1e3:.1f} ms); "
+                       f"{os.uname().machine} {cpu_model()}")}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown cpu"
+
+
+def load_traffic(workload: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), committed under
+    profiles/; null if no measurement exists."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="gemm_4096")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the GEMM shards by output row panels with no exchange, see DESIGN.md",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from mini_triton_nvgpu_v1_amd import configs
+
+    device = torch.device("cuda:0")
+    w = configs.BY_NAME[args.workload]
+    log(f"bench: workload {w.name} {w.M}x{w.N}x{w.K} steps={args.steps} warmup={args.warmup}")
+    r = time_workload(w, args.steps, args.warmup, device)
+    if not r["finite"]:
+        log("bench: non-finite output")
+        return 1
+    ms_per_step = r["wall_s"] * 1e3 / args.steps
+    value = w.flop * args.steps / r["wall_s"] / 1e12
+    avg_kernel_ms = statistics.mean(r["kernel_ms"])
+    achieved = w.flop / (avg_kernel_ms * 1e-3) / 1e12
+    log(f"bench: {r['kernel']} wall {ms_per_step * 1e3:.1f} us/step, "
+        f"kernel avg {avg_kernel_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s")
+
+    extra = {}
+    if not args.no_extra:
+        for other in configs.ALL:
+            if other.name == w.name:
+                continue
+            steps = 200 if other.flop < 1e9 else (50 if other.flop < 2e11 else 10)
+            o = time_workload(other, steps, 5, device)
+            kern_us = statistics.median(o["kernel_ms"]) * 1e3
+            wall_us = o["wall_s"] * 1e6 / steps
+            extra[other.name] = {
+                "us_per_launch_wall": round(wall_us, 2),
+                "us_per_launch_kernel_median": round(kern_us, 2),
+                "tflops_kernel": round(other.flop / (kern_us * 1e-6) / 1e12, 2),
+                "frac_mfma_peak": round(other.flop / (kern_us * 1e-6) / 1e12 / PEAK_TFLOPS_F16, 4),
+                "kernel": o["kernel"], "finite": o["finite"]}
+            log(f"bench: {other.name}: {extra[other.name]}")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w)
+        log(f"bench: cpu baseline {cpu}")
+
+    line = {
+        "metric": "TFLOP/s + % FP16 MFMA peak, 4096^3 f16 GEMM; us/launch small shapes",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (device SplitMix64 seeded N(0,1)/sqrt(K) f16)",
+        "frac_of_peak": round(value / PEAK_TFLOPS_F16, 4),
+        "config": {"workload": w.name, "M": w.M, "N": w.N, "K": w.K,
+                   "tile": list(w.block), "num_waves": w.num_waves,
+                   "group_m": w.group_m, "split_k": w.split_k,
+                   "persistent": w.persistent, "c_dtype": "f16",
+                   "accumulate": "f32", "kernel": r["kernel"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
+                     "peak": PEAK_TFLOPS_F16, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TFLOPS_F16, 4),
+                     "traffic": load_traffic(w.name)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,144 @@
+/*
+ * tb_gfx950 -- C ABI of the MI355X (gfx950) backend for the tb.matmul GEMM
+ * compiler path.
+ *
+ * The reference (zrqnwu/mini_triton_nvgpu_v1) hands a kernel from its
+ * compiler to its launcher as process + text: `tb-opt` lowers the plan-
+ * annotated module to PTX (lib/Transforms/Stage1Pipelines.cpp:101-120,
+ * tools/tb-opt.cpp:11-24), an extractor pulls the binary out, and an external
+ * driver calls cuModuleLoadData + cuLaunchKernel("kernel_tb_kernel_0",
+ * grid, block = num_warps*32) (tools/bench_stage1_fair.py:547-563, :665-699).
+ * This library replaces everything from tb-lower-pipeline-to-nvgpu
+ * (lib/Transforms/LowerPipelineToNVGPU.cpp:2624-2732) downward: the plan
+ * pipeline's finished KernelContract is flattened into a tb_gemm_config and
+ * launched on hand-written gfx950 MFMA kernels.
+ *
+ * Conventions:
+ *  - every int-returning function returns 0 on success, < 0 on error; the
+ *    message is available from tb_last_error() (thread-local);
+ *  - A, B, C and the workspace are caller-owned device pointers, row-major,
+ *    A = M x K f16, B = K x N f16, C = M x N (f16 or f32) with leading
+ *    dimensions from the descriptor;
+ *  - `stream` is a hipStream_t (NULL = the null stream); launches are
+ *    asynchronous and stream-ordered;
+ *  - a tb_gemm_desc is immutable after creation and may be shared between
+ *    threads.
+ */
+#ifndef TB_GFX950_H
+#define TB_GFX950_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TB_GFX950_ABI_VERSION 1
+
+/* element types (reference ScalarKind, include/tb/Analysis/KernelConfig.h:13-16) */
+#define TB_DTYPE_F16 0
+#define TB_DTYPE_F32 1
+
+/* accumulator initialisation (reference AccumulatorInitMode,
+ * include/tb/Analysis/EpiloguePlan.h:16-20): Zero, or DirectGlobalVector =
+ * load C first (the reference's C += A*B) */
+#define TB_ACC_INIT_ZERO 0
+#define TB_ACC_INIT_LOAD_C 1
+
+/* program mapping (reference ProgramMappingKind,
+ * include/tb/Analysis/ProgramMappingPlan.h:19-24, plus the grouped persistent
+ * order this backend adds) */
+#define TB_MAP_TILE 0
+#define TB_MAP_GROUPED_TILE 1
+#define TB_MAP_SPLIT_K 2
+#define TB_MAP_PERSISTENT_TILE 3
+#define TB_MAP_PERSISTENT_GROUPED 4
+
+/* split-K reduction (reference ReductionPlanKind,
+ * include/tb/Analysis/ReductionPlan.h:15-19): SplitKSerial is realised as a
+ * global f32 workspace reduced in fixed split order (deterministic);
+ * SplitKAtomic adds each split into f32 C with atomics */
+#define TB_RED_NONE 0
+#define TB_RED_WORKSPACE 1
+#define TB_RED_ATOMIC 2
+
+/* Flattened KernelContract: everything the gfx950 kernels consume. Mirrors
+ * the fields the reference's lowering reads out of the plans
+ * (LoweringContract, lib/Transforms/LowerPipelineToNVGPU.cpp:45-113). */
+typedef struct tb_gemm_config {
+  int64_t m, n, k;       /* problem shape (KernelConfig problemM/N/K) */
+  int64_t lda, ldb, ldc; /* leading dimensions in elements */
+  int32_t c_dtype;       /* TB_DTYPE_F16 | TB_DTYPE_F32 (A, B are f16) */
+  int32_t acc_init;      /* TB_ACC_INIT_* */
+  int64_t block_m, block_n, block_k; /* macro tile (tileM/N/K) */
+  int64_t num_waves;     /* wavefronts per workgroup (tb.num-warps) */
+  int64_t wave_grid_m, wave_grid_n; /* WarpDecompositionPlan warpGrid */
+  int64_t stages;        /* LDS stages (requested stages) */
+  int32_t mapping;       /* TB_MAP_* */
+  int64_t group_m;       /* grouped order width (GROUP_M) */
+  int64_t split_k;       /* split count (1 = none) */
+  int32_t reduction;     /* TB_RED_* */
+  int64_t num_programs;  /* workgroups launched (persistent: resident) */
+  int32_t xcd_remap;     /* >1: remap program ids so neighbours share an XCD */
+} tb_gemm_config;
+
+typedef struct tb_gemm_desc tb_gemm_desc;
+
+/* Thread-local message of the last failing call ("" if none). */
+const char *tb_last_error(void);
+
+/* Build a descriptor from a flattened config; selects the gfx950 kernel
+ * instance. Replaces LowerPipelineToNVGPU.cpp:2624-2732 (contract
+ * validation + gpu.func emission). */
+int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out);
+
+/* Run the unchanged tb plan pipeline (tb-verify-scope ... tb-cleanup-pipeline,
+ * lib/Transforms/Stage1Pipelines.cpp:14-41) on a module holding one
+ * tb.matmul, with tb-attach-target-info{gpu-arch=<gpu_arch>}, then flatten
+ * the KernelContract (lib/Analysis/KernelContract.cpp:9-65) into a
+ * descriptor. Leading dimensions default to the memref shapes. */
+int tb_plan_from_mlir(const char *mlir, size_t len, const char *gpu_arch,
+                      tb_gemm_desc **out);
+
+/* Read the descriptor side-file that `tb-opt
+ * --tb-lower-pipeline-to-gfx950=desc-file=<path>` writes (replaces the
+ * extracted gpu.binary payload, tools/bench_stage1_fair.py:531-564). */
+int tb_plan_from_file(const char *path, tb_gemm_desc **out);
+
+/* Copy the flattened config back out. */
+int tb_desc_get_config(const tb_gemm_desc *desc, tb_gemm_config *out);
+/* Name of the selected kernel instance (valid while desc lives). */
+const char *tb_desc_kernel_name(const tb_gemm_desc *desc);
+/* Static LDS bytes per workgroup of the selected instance. */
+int64_t tb_desc_lds_bytes(const tb_gemm_desc *desc);
+
+/* Bytes of caller-provided global workspace tb_gemm_launch needs (split-K
+ * f32 partials: split_k * m * n * 4; 0 otherwise). Reference analogue:
+ * ReductionPlan scratchBytes (lib/Analysis/ReductionPlan.cpp:158-177). */
+size_t tb_workspace_bytes(const tb_gemm_desc *desc);
+
+/* Enqueue C = A*B (or C += A*B for TB_ACC_INIT_LOAD_C) on `stream`. */
+int tb_gemm_launch(const tb_gemm_desc *desc, const void *a, const void *b,
+                   void *c, void *workspace, void *stream);
+
+void tb_desc_free(tb_gemm_desc *desc);
+
+/* Harness helper (no reference counterpart: the reference's external driver
+ * owns its inputs, tools/bench_stage1_fair.py:385-404). Fills a rows x cols
+ * f16 matrix (leading dimension ld) on the device: element (r, c) is the
+ * SplitMix64 draw r*cols + c of `seed`, uniform[-1,1) (dist 0) or
+ * Box-Muller normal (dist 1), times `scale`, rounded to nearest even. */
+int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
+                       uint64_t seed, int32_t dist, double scale, void *stream);
+
+/* Number of compiled kernel instances and the name of instance i. */
+int tb_kernel_count(void);
+const char *tb_kernel_name(int i);
+
+int tb_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TB_GFX950_H */

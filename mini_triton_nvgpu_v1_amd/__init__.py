@@ -1,0 +1,216 @@
+"""MI355X (gfx950) backend for the tb.matmul GEMM compiler path.
+
+Python host layer over the C ABI in ``include/tb_gfx950.h`` (library
+``lib/libtb_gfx950.so``, built in-tree by ``make -C mini_triton_nvgpu_v1_amd``).
+The reference's user surface is the ``tb-opt`` driver plus an external
+launcher (``tools/bench_stage1_fair.py:531-564``, ``:665-699``); here
+:func:`plan_from_mlir` runs the same plan pipeline in-process and
+:meth:`GemmDesc.launch` enqueues the gfx950 kernel on a HIP stream.
+
+There is no CPU fallback: every entry point raises if the HIP library is
+missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+__all__ = [
+    "GemmConfig", "GemmDesc", "TbError", "lib", "build", "plan_from_mlir",
+    "plan_from_file", "fill_seeded_f16", "kernel_names", "LIB_PATH", "TB_OPT",
+    "DTYPE_F16", "DTYPE_F32", "ACC_INIT_ZERO", "ACC_INIT_LOAD_C", "MAP_TILE",
+    "MAP_GROUPED_TILE", "MAP_SPLIT_K", "MAP_PERSISTENT_TILE",
+    "MAP_PERSISTENT_GROUPED", "RED_NONE", "RED_WORKSPACE", "RED_ATOMIC",
+]
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libtb_gfx950.so")
+TB_OPT = os.path.join(PKG_DIR, "bin", "tb-opt")
+
+DTYPE_F16, DTYPE_F32 = 0, 1
+ACC_INIT_ZERO, ACC_INIT_LOAD_C = 0, 1
+(MAP_TILE, MAP_GROUPED_TILE, MAP_SPLIT_K, MAP_PERSISTENT_TILE,
+ MAP_PERSISTENT_GROUPED) = range(5)
+RED_NONE, RED_WORKSPACE, RED_ATOMIC = 0, 1, 2
+
+
+class TbError(RuntimeError):
+    """An error reported by libtb_gfx950 (tb_last_error())."""
+
+
+class GemmConfig(ctypes.Structure):
+    """Mirror of ``tb_gemm_config`` (include/tb_gfx950.h)."""
+    _fields_ = [
+        ("m", ctypes.c_int64), ("n", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+        ("c_dtype", ctypes.c_int32), ("acc_init", ctypes.c_int32),
+        ("block_m", ctypes.c_int64), ("block_n", ctypes.c_int64),
+        ("block_k", ctypes.c_int64), ("num_waves", ctypes.c_int64),
+        ("wave_grid_m", ctypes.c_int64), ("wave_grid_n", ctypes.c_int64),
+        ("stages", ctypes.c_int64), ("mapping", ctypes.c_int32),
+        ("group_m", ctypes.c_int64), ("split_k", ctypes.c_int64),
+        ("reduction", ctypes.c_int32), ("num_programs", ctypes.c_int64),
+        ("xcd_remap", ctypes.c_int32),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the backend in-tree (make always runs; it rebuilds what changed)."""
+    jobs = str(min(16, os.cpu_count() or 4))
+    subprocess.run(["make", "-s", "-j" + jobs, "-C", PKG_DIR], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    """Load libtb_gfx950.so; raises TbError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise TbError(
+            f"{LIB_PATH} is missing: build the gfx950 backend first "
+            "(make -C mini_triton_nvgpu_v1_amd, or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    pdesc = ctypes.POINTER(vp)
+    L.tb_last_error.restype = ctypes.c_char_p
+    L.tb_last_error.argtypes = []
+    L.tb_abi_version.restype = ctypes.c_int
+    L.tb_desc_create.argtypes = [ctypes.POINTER(GemmConfig), pdesc]
+    L.tb_desc_create.restype = ctypes.c_int
+    L.tb_plan_from_mlir.argtypes = [ctypes.c_char_p, ctypes.c_size_t,
+                                    ctypes.c_char_p, pdesc]
+    L.tb_plan_from_mlir.restype = ctypes.c_int
+    L.tb_plan_from_file.argtypes = [ctypes.c_char_p, pdesc]
+    L.tb_plan_from_file.restype = ctypes.c_int
+    L.tb_desc_get_config.argtypes = [vp, ctypes.POINTER(GemmConfig)]
+    L.tb_desc_get_config.restype = ctypes.c_int
+    L.tb_desc_kernel_name.argtypes = [vp]
+    L.tb_desc_kernel_name.restype = ctypes.c_char_p
+    L.tb_desc_lds_bytes.argtypes = [vp]
+    L.tb_desc_lds_bytes.restype = i64
+    L.tb_workspace_bytes.argtypes = [vp]
+    L.tb_workspace_bytes.restype = ctypes.c_size_t
+    L.tb_gemm_launch.argtypes = [vp, vp, vp, vp, vp, vp]
+    L.tb_gemm_launch.restype = ctypes.c_int
+    L.tb_desc_free.argtypes = [vp]
+    L.tb_desc_free.restype = None
+    L.tb_fill_seeded_f16.argtypes = [vp, i64, i64, i64, ctypes.c_uint64, i32,
+                                     ctypes.c_double, vp]
+    L.tb_fill_seeded_f16.restype = ctypes.c_int
+    L.tb_kernel_count.restype = ctypes.c_int
+    L.tb_kernel_name.argtypes = [ctypes.c_int]
+    L.tb_kernel_name.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise TbError(lib().tb_last_error().decode())
+
+
+def _ptr(x) -> int | None:
+    """Device address of a torch tensor, an int address, or None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream_handle(stream) -> int | None:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream  # torch.cuda.Stream -> hipStream_t
+
+
+class GemmDesc:
+    """Owning handle of a ``tb_gemm_desc``."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    @classmethod
+    def from_config(cls, cfg: GemmConfig | None = None, **fields) -> "GemmDesc":
+        if cfg is None:
+            cfg = GemmConfig(**fields)
+        h = ctypes.c_void_p()
+        _check(lib().tb_desc_create(ctypes.byref(cfg), ctypes.byref(h)))
+        return cls(h.value)
+
+    @property
+    def handle(self) -> int:
+        return self._h.value
+
+    @property
+    def config(self) -> GemmConfig:
+        cfg = GemmConfig()
+        _check(lib().tb_desc_get_config(self._h, ctypes.byref(cfg)))
+        return cfg
+
+    @property
+    def kernel_name(self) -> str:
+        return lib().tb_desc_kernel_name(self._h).decode()
+
+    @property
+    def lds_bytes(self) -> int:
+        return lib().tb_desc_lds_bytes(self._h)
+
+    @property
+    def workspace_bytes(self) -> int:
+        return lib().tb_workspace_bytes(self._h)
+
+    def launch(self, a, b, c, workspace=None, stream=None) -> None:
+        """Enqueue C = A*B (or C += A*B) for device tensors/addresses."""
+        _check(lib().tb_gemm_launch(self._h, _ptr(a), _ptr(b), _ptr(c),
+                                    _ptr(workspace), _stream_handle(stream)))
+
+    def close(self) -> None:
+        if self._h and self._h.value:
+            lib().tb_desc_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def plan_from_mlir(text: str, gpu_arch: str = "gfx950") -> GemmDesc:
+    """Run the tb plan pipeline on a module holding one tb.matmul."""
+    data = text.encode()
+    h = ctypes.c_void_p()
+    _check(lib().tb_plan_from_mlir(data, len(data), gpu_arch.encode(),
+                                   ctypes.byref(h)))
+    return GemmDesc(h.value)
+
+
+def plan_from_file(path: str) -> GemmDesc:
+    """Load the descriptor side-file written by tb-lower-pipeline-to-gfx950."""
+    h = ctypes.c_void_p()
+    _check(lib().tb_plan_from_file(path.encode(), ctypes.byref(h)))
+    return GemmDesc(h.value)
+
+
+def fill_seeded_f16(dst, rows: int, cols: int, seed: int, dist: int = 0,
+                    scale: float = 1.0, ld: int | None = None,
+                    stream=None) -> None:
+    """Device-side seeded f16 fill (SplitMix64; dist 0 uniform, 1 normal)."""
+    _check(lib().tb_fill_seeded_f16(_ptr(dst), rows, cols,
+                                    cols if ld is None else ld, seed, dist,
+                                    scale, _stream_handle(stream)))
+
+
+def kernel_names() -> list[str]:
+    L = lib()
+    return [L.tb_kernel_name(i).decode() for i in range(L.tb_kernel_count())]

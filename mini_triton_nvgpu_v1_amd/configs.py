@@ -1,0 +1,125 @@
+"""The five benchmark/parity workloads of the tb.matmul gfx950 path.
+
+Each workload is a ``tb.matmul`` module (the reference's own input format,
+``examples/*.mlir``) plus the seeded-input recipe. Shapes follow
+``examples/smoke_64x64x32.mlir``, ``examples/smoke_96x80x32.mlir``,
+``examples/smoke_128x128x32.mlir``, and scaled-up versions of
+``examples/smoke_splitk_64x64x64.mlir`` and
+``examples/smoke_persistent_192x128x32.mlir``. Unlike the reference
+(f32 C, C += A*B) these write f16 C = A*B with f32 accumulation.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from . import (ACC_INIT_ZERO, DTYPE_F16, MAP_GROUPED_TILE,
+               MAP_PERSISTENT_GROUPED, MAP_SPLIT_K, MAP_TILE, RED_NONE,
+               RED_WORKSPACE, GemmConfig)
+
+UNIFORM, NORMAL = 0, 1
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    M: int
+    N: int
+    K: int
+    seed: int
+    dist: int
+    block: tuple  # (block_m, block_n, block_k)
+    num_waves: int
+    stages: int = 2
+    group_m: int = 8
+    exact_tile: bool = True
+    split_k: int = 1
+    persistent: bool = False
+    num_ctas: int = 1
+    module_attrs: dict = field(default_factory=dict)
+
+    @property
+    def flop(self) -> int:
+        return 2 * self.M * self.N * self.K
+
+    @property
+    def scale(self) -> float:
+        return 1.0 / math.sqrt(self.K) if self.dist == NORMAL else 1.0
+
+    @property
+    def seed_b(self) -> int:
+        return self.seed ^ 0xB
+
+    def mlir(self, c_type: str = "f16") -> str:
+        """The tb.matmul module fed to the plan pipeline."""
+        attrs = {"tb.num-warps": f"{self.num_waves} : i64",
+                 "tb.requested-stages": f"{self.stages} : i64"}
+        if self.split_k > 1:
+            attrs["tb.split-k"] = f"{self.split_k} : i64"
+            attrs["tb.reduction-mode"] = '"split_k_serial"'
+        if self.persistent:
+            attrs["tb.persistent"] = "true"
+            attrs["tb.num-ctas"] = f"{self.num_ctas} : i64"
+        attrs.update(self.module_attrs)
+        mattr = ", ".join(f'"{k}" = {v}' for k, v in attrs.items())
+        bm, bn, bk = self.block
+        M, N, K = self.M, self.N, self.K
+        a, b, c = (f"memref<{M}x{K}xf16>", f"memref<{K}x{N}xf16>",
+                   f"memref<{M}x{N}x{c_type}>")
+        gm = f",\n                          group_m = {self.group_m} : i64"
+        return (
+            f"module attributes {{{mattr}}} {{\n"
+            f"  func.func @kernel(%A: {a}, %B: {b},\n"
+            f"                    %C: {c}) {{\n"
+            f"    tb.matmul %A, %B, %C {{block_m = {bm} : i64, block_n = {bn} : i64,\n"
+            f"                          block_k = {bk} : i64, exact_tile = "
+            f"{'true' if self.exact_tile else 'false'}{gm}}}\n"
+            f"      : {a}, {b}, {c}\n"
+            f"    func.return\n"
+            f"  }}\n"
+            f"}}\n")
+
+    def direct_config(self) -> GemmConfig:
+        """Flattened descriptor equivalent to what the plan pipeline derives."""
+        bm, bn, bk = self.block
+        wg = {1: (1, 1), 2: (2, 1), 4: (2, 2), 8: (2, 4)}[self.num_waves]
+        tiles_m, tiles_n = -(-self.M // bm), -(-self.N // bn)
+        if self.persistent:
+            mapping = MAP_PERSISTENT_GROUPED
+            programs = min(self.num_ctas, tiles_m * tiles_n)
+        elif self.split_k > 1:
+            mapping = MAP_SPLIT_K
+            programs = tiles_m * tiles_n * self.split_k
+        elif self.group_m > 1 and tiles_m > 1 and tiles_n > 1:
+            mapping = MAP_GROUPED_TILE
+            programs = tiles_m * tiles_n
+        else:
+            mapping = MAP_TILE
+            programs = tiles_m * tiles_n
+        return GemmConfig(
+            m=self.M, n=self.N, k=self.K, lda=self.K, ldb=self.N, ldc=self.N,
+            c_dtype=DTYPE_F16, acc_init=ACC_INIT_ZERO, block_m=bm, block_n=bn,
+            block_k=bk, num_waves=self.num_waves, wave_grid_m=wg[0],
+            wave_grid_n=wg[1], stages=self.stages, mapping=mapping,
+            group_m=self.group_m if mapping != MAP_TILE else 1,
+            split_k=self.split_k,
+            reduction=RED_WORKSPACE if self.split_k > 1 else RED_NONE,
+            num_programs=programs, xcd_remap=8)
+
+
+SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,
+                 (64, 64, 32), num_waves=4)
+RAGGED = Workload("ragged_96x80x32", 96, 80, 32, 0x5EED0002, UNIFORM,
+                  (64, 64, 32), num_waves=4, exact_tile=False)
+RAGGED_128 = Workload("tile_128x128x32", 128, 128, 32, 0x5EED0003, UNIFORM,
+                      (128, 128, 32), num_waves=4)
+ROOFLINE = Workload("gemm_4096", 4096, 4096, 4096, 0x5EED0004, NORMAL,
+                    (256, 256, 64), num_waves=4, stages=2, group_m=8)
+SPLIT_K = Workload("splitk_512x512x16384", 512, 512, 16384, 0x5EED0005,
+                   UNIFORM, (128, 128, 64), num_waves=4, split_k=8)
+PERSISTENT = Workload("persistent_8192", 8192, 8192, 8192, 0x5EED0006, NORMAL,
+                      (256, 256, 64), num_waves=4, group_m=8, persistent=True,
+                      num_ctas=256)
+
+ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]
+BY_NAME = {w.name: w for w in ALL}

@@ -1,0 +1,182 @@
+// Auxiliary gfx950 kernels of the tb.matmul path:
+//  * the deterministic split-K reduction (global f32 workspace summed in
+//    fixed split order, then cast) that realises the reference's
+//    SplitKSerial reduction plan (lib/Analysis/ReductionPlan.cpp:136-193),
+//    which the reference itself never lowers (LowerPipelineToNVGPU.cpp:803-810);
+//  * the seeded f16 input generator used by the benchmark harness.
+// Also aggregates the GEMM instance registry.
+#include "gemm_gfx950.h"
+
+#include <math.h>
+
+namespace tbk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct ReduceArgs {
+  const float *ws;
+  void *C;
+  int M, N, ldc, split_k;
+  int c_f16;
+  int load_c;
+};
+
+// One thread per 4 consecutive columns (N % 4 == 0 is required by the host).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs a) {
+  const int cols4 = a.N / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.M * cols4)
+    return;
+  const int row = (int)(idx / cols4), col = (int)(idx % cols4) * 4;
+  const size_t plane = (size_t)a.M * (size_t)a.N;
+  const f32x4 *src =
+      reinterpret_cast<const f32x4 *>(a.ws + (size_t)row * a.N + col);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if (a.load_c && !a.c_f16)
+    s = *reinterpret_cast<const f32x4 *>(reinterpret_cast<float *>(a.C) +
+                                          (size_t)row * a.ldc + col);
+  for (int p = 0; p < a.split_k; ++p) // fixed order: deterministic result
+    s += src[p * (plane / 4)];
+  if (a.c_f16) {
+    _Float16 *c = reinterpret_cast<_Float16 *>(a.C) + (size_t)row * a.ldc + col;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
+    *reinterpret_cast<h4 *>(c) = h;
+  } else {
+    *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(a.C) +
+                               (size_t)row * a.ldc + col) = s;
+  }
+}
+
+// ---- seeded inputs -------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// binary64 -> binary16, round to nearest even, from the bit pattern.
+__device__ uint16_t f64_to_f16_bits(double x) {
+  const uint64_t b = __double_as_longlong(x);
+  const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+  const int exp = (int)((b >> 52) & 0x7ff);
+  const uint64_t frac = b & 0xFFFFFFFFFFFFFull;
+  if (exp == 0x7ff)
+    return frac ? (uint16_t)(sign | 0x7e00u) : (uint16_t)(sign | 0x7c00u);
+  if (exp == 0)
+    return sign;
+  int e = exp - 1023;
+  const uint64_t m = frac | (1ull << 52);
+  if (e >= 16)
+    return (uint16_t)(sign | 0x7c00u);
+  if (e >= -14) {
+    uint64_t q = m >> 42;
+    const uint64_t rem = m & ((1ull << 42) - 1), half = 1ull << 41;
+    if (rem > half || (rem == half && (q & 1)))
+      q++;
+    if (q == 0x800) {
+      q = 0x400;
+      e++;
+    }
+    if (e >= 16)
+      return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint16_t)(e + 15) << 10) | (uint16_t)(q & 0x3ff));
+  }
+  const int shift = 28 - e;
+  if (shift > 54)
+    return sign;
+  uint64_t q = m >> shift;
+  const uint64_t rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+  if (rem > half || (rem == half && (q & 1)))
+    q++;
+  return (uint16_t)(sign | (uint16_t)q);
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(uint16_t *dst, int64_t rows,
+                                                   int64_t cols, int64_t ld,
+                                                   uint64_t seed, int dist,
+                                                   double scale) {
+  const int64_t n = rows * cols;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = idx / cols, c = idx % cols;
+    double v;
+    if (dist == 1) {
+      const uint64_t x1 = splitmix64_at(seed, 2 * (uint64_t)idx);
+      const uint64_t x2 = splitmix64_at(seed, 2 * (uint64_t)idx + 1);
+      const double u1 = (double)((x1 >> 11) + 1) * (1.0 / 9007199254740992.0);
+      const double u2 = (double)(x2 >> 11) * (1.0 / 9007199254740992.0);
+      v = sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925286766559 * u2);
+    } else {
+      const uint64_t x = splitmix64_at(seed, (uint64_t)idx);
+      v = (double)(x >> 40) * (1.0 / 16777216.0) * 2.0 - 1.0;
+    }
+    dst[r * ld + c] = f64_to_f16_bits(v * scale);
+  }
+}
+
+hipError_t launch_reduce_ex(const float *ws, void *C, int M, int N, int ldc,
+                            int split_k, int c_f16, int load_c, hipStream_t s) {
+  ReduceArgs a{ws, C, M, N, ldc, split_k, c_f16, load_c};
+  const int64_t threads = (int64_t)M * (N / 4);
+  const int blocks = (int)((threads + 255) / 256);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
+                       uint64_t seed, int dist, double scale, hipStream_t s) {
+  const int64_t n = rows * cols;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536)
+    blocks = 65536;
+  if (blocks < 1)
+    blocks = 1;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     reinterpret_cast<uint16_t *>(dst), rows, cols, ld, seed,
+                     dist, scale);
+  return hipGetLastError();
+}
+
+// ---- instance registry ----------------------------------------------------
+const KernelEntry *entries_small(int *n);
+const KernelEntry *entries_mid(int *n);
+const KernelEntry *entries_large(int *n);
+
+static const KernelEntry *(*const kTables[])(int *) = {entries_small, entries_mid,
+                                                       entries_large};
+
+int kernel_count() {
+  int total = 0;
+  for (auto t : kTables) {
+    int n = 0;
+    t(&n);
+    total += n;
+  }
+  return total;
+}
+
+const KernelEntry *kernel_at(int i) {
+  for (auto t : kTables) {
+    int n = 0;
+    const KernelEntry *e = t(&n);
+    if (i < n)
+      return e + i;
+    i -= n;
+  }
+  return nullptr;
+}
+
+const KernelEntry *find_kernel(const KernelKey &k) {
+  const int n = kernel_count();
+  for (int i = 0; i < n; ++i) {
+    const KernelEntry *e = kernel_at(i);
+    if (e->key.bm == k.bm && e->key.bn == k.bn && e->key.bk == k.bk &&
+        e->key.wgm == k.wgm && e->key.wgn == k.wgn && e->key.out == k.out)
+      return e;
+  }
+  return nullptr;
+}
+
+} // namespace tbk

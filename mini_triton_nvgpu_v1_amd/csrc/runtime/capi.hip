@@ -1,0 +1,261 @@
+// C ABI of the gfx950 backend (include/tb_gfx950.h): descriptor creation,
+// kernel-instance selection and stream-ordered launch.
+//
+// Replaces the reference's lowering entry (TBLowerPipelineToNVGPU,
+// lib/Transforms/LowerPipelineToNVGPU.cpp:2624-2732: parseKernelContract ->
+// validateLoweringContract -> gpu.func) and its external launcher
+// (cuLaunchKernel with grid = programs, block = num_warps*32,
+// tools/bench_stage1_fair.py:665-699). Here block = num_waves*64 and the
+// kernel is a precompiled gfx950 instance chosen by tile shape.
+#include "tb_gfx950.h"
+
+#include "../kernels/gemm_gfx950.h"
+#include "desc.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <limits>
+#include <string>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const std::string &msg) {
+  g_last_error = msg;
+  return -1;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess)
+    return 0;
+  return fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+} // namespace
+
+namespace tbrt {
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+// Validate a flattened config and bind it to a compiled instance.
+int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
+  if (!out)
+    return fail("tb_desc_create: out is NULL");
+  *out = nullptr;
+  if (c.m <= 0 || c.n <= 0 || c.k <= 0)
+    return fail("problem M/N/K must be positive");
+  if (c.lda < c.k || c.ldb < c.n || c.ldc < c.n)
+    return fail("leading dimensions must cover the row lengths (lda >= K, "
+                "ldb >= N, ldc >= N)");
+  if (c.k % 8 || c.n % 8 || c.lda % 8 || c.ldb % 8 || c.ldc % 8)
+    return fail("gfx950 16-byte row transport requires K, N and every "
+                "leading dimension to be multiples of 8 elements");
+  if (c.c_dtype != TB_DTYPE_F16 && c.c_dtype != TB_DTYPE_F32)
+    return fail("c_dtype must be TB_DTYPE_F16 or TB_DTYPE_F32");
+  if (c.acc_init != TB_ACC_INIT_ZERO && c.acc_init != TB_ACC_INIT_LOAD_C)
+    return fail("acc_init must be TB_ACC_INIT_ZERO or TB_ACC_INIT_LOAD_C");
+  if (c.acc_init == TB_ACC_INIT_LOAD_C && c.c_dtype != TB_DTYPE_F32)
+    return fail("accumulating into C (C += A*B) requires f32 C");
+  if (c.block_m <= 0 || c.block_n <= 0 || c.block_k <= 0)
+    return fail("block M/N/K must be positive");
+  if (c.wave_grid_m * c.wave_grid_n != c.num_waves)
+    return fail("wave grid must multiply to num_waves");
+  if (c.split_k < 1)
+    return fail("split_k must be >= 1");
+  if (c.group_m < 1)
+    return fail("group_m must be >= 1");
+  const int64_t tiles_m = ceil_div(c.m, c.block_m);
+  const int64_t tiles_n = ceil_div(c.n, c.block_n);
+  const int64_t tiles_k = ceil_div(c.k, c.block_k);
+  int64_t total_work = tiles_m * tiles_n;
+  int out_mode = tbk::kOutF16;
+  switch (c.mapping) {
+  case TB_MAP_TILE:
+  case TB_MAP_GROUPED_TILE:
+  case TB_MAP_PERSISTENT_TILE:
+  case TB_MAP_PERSISTENT_GROUPED:
+    if (c.split_k != 1 || c.reduction != TB_RED_NONE)
+      return fail("tile/grouped/persistent mappings carry no split-K reduction");
+    if (c.c_dtype == TB_DTYPE_F16)
+      out_mode = tbk::kOutF16;
+    else
+      out_mode = c.acc_init == TB_ACC_INIT_LOAD_C ? tbk::kOutF32Accum
+                                                  : tbk::kOutF32Partial;
+    if (c.c_dtype == TB_DTYPE_F32 && c.acc_init == TB_ACC_INIT_ZERO &&
+        c.ldc > std::numeric_limits<int>::max())
+      return fail("ldc too large");
+    break;
+  case TB_MAP_SPLIT_K:
+    if (c.split_k < 2)
+      return fail("split_k mapping requires split_k >= 2");
+    total_work = tiles_m * tiles_n * c.split_k;
+    if (c.reduction == TB_RED_WORKSPACE) {
+      out_mode = tbk::kOutF32Partial;
+    } else if (c.reduction == TB_RED_ATOMIC) {
+      if (c.c_dtype != TB_DTYPE_F32 || c.acc_init != TB_ACC_INIT_LOAD_C)
+        return fail("atomic split-K accumulates into f32 C (C += A*B)");
+      out_mode = tbk::kOutF32Atomic;
+    } else {
+      return fail("split_k mapping requires a reduction");
+    }
+    break;
+  default:
+    return fail("unknown mapping kind");
+  }
+  const bool persistent = c.mapping == TB_MAP_PERSISTENT_TILE ||
+                          c.mapping == TB_MAP_PERSISTENT_GROUPED;
+  int64_t programs = persistent ? c.num_programs : total_work;
+  if (persistent && (programs <= 0 || programs > total_work))
+    programs = std::min<int64_t>(total_work, programs <= 0 ? 256 : programs);
+  if (!persistent && c.num_programs > 0 && c.num_programs != total_work)
+    return fail("num_programs disagrees with the mapping's launch formula");
+
+  // every operand must span fewer than 2^31 bytes (32-bit buffer offsets)
+  const int64_t lim = (int64_t)1 << 31;
+  if (c.m * c.lda * 2 >= lim || c.k * c.ldb * 2 >= lim ||
+      c.m * c.ldc * (c.c_dtype == TB_DTYPE_F16 ? 2 : 4) >= lim ||
+      (c.reduction == TB_RED_WORKSPACE && c.split_k * c.m * c.n * 4 >= lim))
+    return fail("operands larger than 2 GiB are not supported by the 32-bit "
+                "buffer addressing of this backend");
+  if (total_work > std::numeric_limits<int>::max())
+    return fail("too many programs");
+
+  tbk::KernelKey key{(int)c.block_m, (int)c.block_n, (int)c.block_k,
+                     (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode};
+  const tbk::KernelEntry *e = tbk::find_kernel(key);
+  if (!e) {
+    char buf[256];
+    snprintf(buf, sizeof buf,
+             "no gfx950 kernel instance for tile %lldx%lldx%lld, wave grid "
+             "%lldx%lld, output mode %d",
+             (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
+             (long long)c.wave_grid_m, (long long)c.wave_grid_n, out_mode);
+    return fail(buf);
+  }
+  tb_gemm_desc *d = new tb_gemm_desc();
+  d->cfg = c;
+  d->cfg.num_programs = programs;
+  d->entry = e;
+  d->out_mode = out_mode;
+  d->tiles_m = tiles_m;
+  d->tiles_n = tiles_n;
+  d->tiles_k = tiles_k;
+  d->total_work = total_work;
+  d->lds_bytes = 2 * (c.block_m + c.block_n) * c.block_k * 2;
+  d->workspace_bytes = c.reduction == TB_RED_WORKSPACE
+                           ? (size_t)(c.split_k * c.m * c.n * 4)
+                           : 0;
+  *out = d;
+  return 0;
+}
+
+} // namespace tbrt
+
+extern "C" {
+
+const char *tb_last_error(void) { return g_last_error.c_str(); }
+
+int tb_abi_version(void) { return TB_GFX950_ABI_VERSION; }
+
+int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out) {
+  if (!cfg)
+    return fail("tb_desc_create: cfg is NULL");
+  return tbrt::create_desc(*cfg, out);
+}
+
+int tb_desc_get_config(const tb_gemm_desc *desc, tb_gemm_config *out) {
+  if (!desc || !out)
+    return fail("tb_desc_get_config: NULL argument");
+  *out = desc->cfg;
+  return 0;
+}
+
+const char *tb_desc_kernel_name(const tb_gemm_desc *desc) {
+  return desc && desc->entry ? desc->entry->name : "";
+}
+
+int64_t tb_desc_lds_bytes(const tb_gemm_desc *desc) {
+  return desc ? desc->lds_bytes : 0;
+}
+
+size_t tb_workspace_bytes(const tb_gemm_desc *desc) {
+  return desc ? desc->workspace_bytes : 0;
+}
+
+void tb_desc_free(tb_gemm_desc *desc) { delete desc; }
+
+int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
+                   void *c, void *workspace, void *stream) {
+  if (!d)
+    return fail("tb_gemm_launch: desc is NULL");
+  if (!a || !b || !c)
+    return fail("tb_gemm_launch: A, B and C must be device pointers");
+  if (d->workspace_bytes && !workspace)
+    return fail("tb_gemm_launch: this descriptor needs a workspace of " +
+                std::to_string(d->workspace_bytes) + " bytes");
+  const tb_gemm_config &cf = d->cfg;
+  tbk::GemmParams p{};
+  p.A = a;
+  p.B = b;
+  p.C = c;
+  p.ws = reinterpret_cast<float *>(workspace);
+  p.M = (int)cf.m;
+  p.N = (int)cf.n;
+  p.K = (int)cf.k;
+  p.lda = (int)cf.lda;
+  p.ldb = (int)cf.ldb;
+  p.ldc = (int)cf.ldc;
+  p.tiles_m = (int)d->tiles_m;
+  p.tiles_n = (int)d->tiles_n;
+  p.tiles_k = (int)d->tiles_k;
+  p.group_m = (int)cf.group_m;
+  p.split_k = (int)cf.split_k;
+  p.mapping = cf.mapping;
+  p.total_work = (int)d->total_work;
+  p.xcds = cf.xcd_remap;
+  p.ws_ld = (int)cf.n;
+  if (d->out_mode == tbk::kOutF32Partial && cf.mapping != TB_MAP_SPLIT_K) {
+    p.ws = reinterpret_cast<float *>(c); // plain f32 store into C
+    p.ws_ld = (int)cf.ldc;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void *args[] = {&p};
+  const dim3 grid((unsigned)cf.num_programs), block((unsigned)(cf.num_waves * 64));
+  if (int rc = check_hip(hipLaunchKernel(d->entry->fn, grid, block, args, 0, s),
+                         "hipLaunchKernel(gemm)"))
+    return rc;
+  if (cf.mapping == TB_MAP_SPLIT_K && cf.reduction == TB_RED_WORKSPACE) {
+    if (int rc = check_hip(
+            tbk::launch_reduce_ex(p.ws, c, p.M, p.N, p.ldc, p.split_k,
+                                  cf.c_dtype == TB_DTYPE_F16 ? 1 : 0,
+                                  cf.acc_init == TB_ACC_INIT_LOAD_C ? 1 : 0, s),
+            "hipLaunchKernel(split-k reduce)"))
+      return rc;
+  }
+  return 0;
+}
+
+int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
+                       uint64_t seed, int32_t dist, double scale, void *stream) {
+  if (!dst || rows < 0 || cols < 0 || ld < cols)
+    return fail("tb_fill_seeded_f16: bad arguments");
+  if (dist != 0 && dist != 1)
+    return fail("tb_fill_seeded_f16: dist must be 0 (uniform) or 1 (normal)");
+  return check_hip(tbk::launch_fill(dst, rows, cols, ld, seed, dist, scale,
+                                    reinterpret_cast<hipStream_t>(stream)),
+                   "hipLaunchKernel(fill)");
+}
+
+int tb_kernel_count(void) { return tbk::kernel_count(); }
+
+const char *tb_kernel_name(int i) {
+  const tbk::KernelEntry *e = tbk::kernel_at(i);
+  return e ? e->name : "";
+}
+
+} // extern "C"

@@ -1,0 +1,99 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+public header declares, and validates descriptors without touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import mini_triton_nvgpu_v1_amd as tb
+from mini_triton_nvgpu_v1_amd import configs
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tb_gfx950.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tb_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = tb.lib()
+    names = declared_functions()
+    assert "tb_gemm_launch" in names and "tb_plan_from_mlir" in names
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in include/tb_gfx950.h but not exported"
+
+
+def test_abi_version_and_struct_layout(tmp_path):
+    """The ctypes mirror of tb_gemm_config matches the C compiler's layout."""
+    assert tb.lib().tb_abi_version() == 1
+    fields = [name for name, _ in tb.GemmConfig._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "tb_gfx950.h"\n'
+        "int main(void) {\n"
+        '  printf("%zu\\n", sizeof(tb_gemm_config));\n'
+        + "".join(f'  printf("%zu\\n", offsetof(tb_gemm_config, {f}));\n' for f in fields)
+        + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    import subprocess
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    out = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True,
+                                          text=True).stdout.split()]
+    assert out[0] == ctypes.sizeof(tb.GemmConfig)
+    assert out[1:] == [getattr(tb.GemmConfig, f).offset for f in fields]
+
+
+def test_kernel_registry_names():
+    names = tb.kernel_names()
+    assert len(names) >= 40
+    assert "tb_gemm_gfx950_256x256x64_w2x2_out0" in names
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_every_workload_has_an_instance(w):
+    d = tb.GemmDesc.from_config(w.direct_config())
+    bm, bn, bk = w.block
+    assert d.kernel_name.startswith(f"tb_gemm_gfx950_{bm}x{bn}x{bk}_")
+    assert d.lds_bytes == 2 * (bm + bn) * bk * 2
+    if w.split_k > 1:
+        assert d.workspace_bytes == w.split_k * w.M * w.N * 4
+    else:
+        assert d.workspace_bytes == 0
+
+
+def _cfg(**kw):
+    c = configs.SMOKE.direct_config()
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(m=0), "positive"),
+    (dict(k=36, lda=36), "multiples of 8"),
+    (dict(lda=16), "leading dimensions"),
+    (dict(wave_grid_m=1), "wave grid"),
+    (dict(block_m=48, num_programs=2), "no gfx950 kernel instance"),
+    (dict(mapping=tb.MAP_SPLIT_K, split_k=1), "split_k >= 2"),
+    (dict(mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_NONE), "reduction"),
+    (dict(mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_ATOMIC), "f32 C"),
+    (dict(acc_init=tb.ACC_INIT_LOAD_C), "f32 C"),
+    (dict(num_programs=7), "launch formula"),
+    (dict(mapping=9), "unknown mapping"),
+])
+def test_descriptor_validation_errors(kw, msg):
+    with pytest.raises(tb.TbError, match=msg):
+        tb.GemmDesc.from_config(_cfg(**kw))
+
+
+def test_launch_argument_errors_before_any_gpu_call():
+    d = tb.GemmDesc.from_config(configs.SPLIT_K.direct_config())
+    with pytest.raises(tb.TbError, match="device pointers"):
+        d.launch(0, 0, 0)
+    with pytest.raises(tb.TbError, match="workspace"):
+        d.launch(16, 16, 16, None)
