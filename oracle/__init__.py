@@ -135,12 +135,17 @@ def check_tolerance(got: np.ndarray, ref: np.ndarray, row_begin: int = 0,
                     rtol: float = 1e-2):
     """Count elements violating |got-ref| <= rtol*(|ref|+1) (NaN counts as bad).
 
+    `got` is the whole M x N result; `ref` holds rows [row_begin,
+    row_begin + ref.shape[0]) of the reference (as returned by gemm_f64).
     Returns (violations, max_abs_err, (worst_row, worst_col))."""
     got = np.ascontiguousarray(got)
     is_f32 = got.dtype == np.float32
     assert is_f32 or got.dtype == np.float16
     N = got.shape[1]
     row_end = row_begin + ref.shape[0]
+    if got.shape[0] < row_end or ref.shape[1] != N:
+        raise ValueError(f"check_tolerance: result has {got.shape} but the "
+                         f"reference covers rows [{row_begin}, {row_end}) x {ref.shape[1]}")
     err = ctypes.c_double()
     wr, wc = ctypes.c_int64(), ctypes.c_int64()
     bad = lib().tbo_check_tolerance(_ptr(got), int(is_f32), N, _ptr(ref), N, N,

@@ -141,6 +141,23 @@ def test_check_tolerance_counts_planted_errors():
     assert bad16 >= 1
 
 
+def test_check_tolerance_row_sample_indexes_absolute_rows():
+    rng = np.random.default_rng(5)
+    A = rng.uniform(-1, 1, (12, 8)).astype(np.float16)
+    B = rng.uniform(-1, 1, (8, 6)).astype(np.float16)
+    full = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    ref = oracle.gemm_f64(A, B, row_begin=5, row_end=9)
+    assert oracle.check_tolerance(full, ref, row_begin=5)[0] == 0
+    planted = full.copy()
+    planted[2, 1] += 5.0  # outside the sampled rows: not counted
+    assert oracle.check_tolerance(planted, ref, row_begin=5)[0] == 0
+    planted[7, 4] += 5.0  # inside: counted at its absolute position
+    bad, _, worst = oracle.check_tolerance(planted, ref, row_begin=5)
+    assert bad == 1 and worst == (7, 4)
+    with pytest.raises(ValueError):
+        oracle.check_tolerance(full[5:9], ref, row_begin=5)  # a slice is refused
+
+
 def test_planted_oracle_mistake_is_caught():
     """A transposed-operand or dropped-term bug in the oracle fails the pin."""
     rng = np.random.default_rng(9)
