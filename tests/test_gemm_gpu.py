@@ -72,7 +72,7 @@ def test_persistent_8192_parity_row_sample(device):
 
 
 RAGGED_SHAPES = [(1, 8, 8), (33, 24, 16), (97, 88, 40), (200, 136, 72),
-                 (65, 64, 32), (64, 72, 96), (130, 260, 264)]
+                 (65, 64, 32), (64, 72, 96), (130, 264, 264)]
 
 
 @pytest.mark.parametrize("M,N,K", RAGGED_SHAPES)
