@@ -19,6 +19,12 @@ static constexpr int kBufferFlags = 0x00020000;
 // guarantees every operand spans fewer than 2^31 bytes.
 static constexpr uint32_t kOob = 0x80000000u;
 
+// sched_group_barrier instruction classes (LLVM AMDGPU)
+static constexpr int kSchedMfma = 0x008;
+static constexpr int kSchedVmemRead = 0x020;
+static constexpr int kSchedDsRead = 0x100;
+static constexpr int kSchedDsWrite = 0x200;
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p,
                                                             uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
@@ -26,9 +32,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p,
 }
 
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r,
-                                            uint32_t off) {
-  return __builtin_bit_cast(u32x4,
-                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+                                            uint32_t voff, int soff) {
+  return __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
 // Physical 16-byte chunk of (row, chunk) in a K-contiguous LDS tile with
@@ -74,10 +80,12 @@ struct GemmTile {
   static constexpr int WTN = BN / WGN;
   static constexpr int TM = WTM / 32;
   static constexpr int TN = WTN / 32;
-  static constexpr int KCH = BK / 8; // 16-byte chunks per LDS row
+  static constexpr int NMFMA = TM * TN; // MFMAs per 16-deep k step per wave
+  static constexpr int KCH = BK / 8;    // 16-byte chunks per LDS row
   static constexpr int KSTEPS = BK / 16;
-  // A: BM*KCH chunks
+  // A: BM*KCH chunks; thread t owns rows t/KCH + i*RS, chunk t%KCH
   static constexpr int NA = BM * KCH / NT;
+  static constexpr int RS = NT / KCH;
   // B: blocks of KB rows x 8 columns, transposed in registers
   static constexpr int KB = ((BK / 8) * (BN / 8) >= NT)   ? 8
                             : ((BK / 4) * (BN / 8) >= NT) ? 4
@@ -88,18 +96,40 @@ struct GemmTile {
   static constexpr int B_STAGE = BN * KCH;
   static constexpr int STAGE = A_STAGE + B_STAGE;
   static constexpr int LDS_BYTES = 2 * STAGE * 16;
+  // k step (within a k-tile) at which the next tile's A / B are written to
+  // LDS and the tile after that is requested from global memory
+  static constexpr int STEP_A = 0;
+  static constexpr int STEP_B = KSTEPS >= 4 ? 1 : 0;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
-  static_assert(BK % 16 == 0 && KCH <= 8, "BK must be 16, 32 or 64");
+  static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
+  static_assert(NT % KCH == 0, "threads per A row chunk");
   static_assert(NA >= 1 && NA * NT == BM * KCH, "A chunks per thread");
   static_assert(NBB >= 1 && NBB * NT == (BK / KB) * (BN / 8), "B blocks");
 };
+
+// Interleave one k step's MFMAs with its memory traffic so the matrix pipe
+// never waits behind a burst of LDS or global instructions.
+template <int NMFMA, int NREAD, int NWRITE, int NVMEM>
+__device__ __forceinline__ void sched_step() {
+#pragma unroll
+  for (int i = 0; i < NMFMA; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    if (i < NREAD)
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    if (i < NWRITE)
+      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+    if (i < NVMEM)
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+  }
+}
 
 template <int BM, int BN, int BK, int WGM, int WGN, int OUT>
 __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   using T = GemmTile<BM, BN, BK, WGM, WGN, OUT>;
   constexpr int NT = T::NT, KCH = T::KCH, NA = T::NA, KB = T::KB,
-                NBB = T::NBB, TM = T::TM, TN = T::TN;
+                NBB = T::NBB, TM = T::TM, TN = T::TN, RS = T::RS,
+                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA;
   __shared__ u32x4 lds[2 * T::STAGE];
 
   const int tid = threadIdx.x;
@@ -119,7 +149,15 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   if (p.xcds > 1 && (nprog % p.xcds) == 0)
     prog = (prog % p.xcds) * (nprog / p.xcds) + prog / p.xcds;
 
-  for (int work = prog; work < p.total_work; work += (persistent ? nprog : p.total_work)) {
+  // per-thread constants of the global -> LDS transport
+  const int a_row0 = tid / KCH, a_c = tid % KCH;
+  const int a_soff_step = RS * p.lda * 2; // bytes between this thread's A rows
+  const int fr_a = wm * T::WTM + (lane & 31); // fragment rows in the A tile
+  const int fr_b = wn * T::WTN + (lane & 31); // fragment rows in the B^T tile
+  const int khalf = lane >> 5;
+
+  for (int work = prog; work < p.total_work;
+       work += (persistent ? nprog : p.total_work)) {
     int tile_m, tile_n, part;
     map_program(p, work, tile_m, tile_n, part);
     int kt0 = 0, nk = p.tiles_k;
@@ -130,6 +168,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       nk = base + (part < extra ? 1 : 0);
     }
     const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int kt_end = kt0 + nk;
 
     f32x16 acc[TM][TN];
 #pragma unroll
@@ -138,19 +177,12 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = (f32x16){};
 
-    // ---- per-thread global coordinates (fixed across the K loop) --------
-    // The k-dependent part of every address is wave-uniform and travels in
-    // the buffer instruction's scalar offset; a row or column outside the
-    // problem gets a vector offset of kOob so the load returns zeros.
-    const int a_kc = (tid % KCH) * 8; // same k chunk for all of this thread's A rows
-    uint32_t a_voff[NA];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int row = (tid + i * NT) / KCH;
-      a_voff[i] = (m0 + row) < p.M
-                      ? ((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)a_kc) * 2u
-                      : kOob;
-    }
+    // The k-dependent part of every global address is wave-uniform and rides
+    // in the buffer instruction's scalar offset. A row, column or k-tile
+    // outside the problem gets the vector offset kOob: the load returns 0.
+    const uint32_t a_voff =
+        ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + (uint32_t)(a_c * 8)) * 2u;
+    const int a_rows_left = p.M - m0 - a_row0; // row i valid iff i*RS < left
     uint32_t b_voff[NBB];
     int b_k[NBB];
 #pragma unroll
@@ -159,42 +191,42 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       const int kb = b / (BN / 8), nb = b % (BN / 8);
       b_k[j] = kb * KB;
       b_voff[j] = (n0 + nb * 8) < p.N
-                      ? ((uint32_t)(kb * KB) * (uint32_t)p.ldb + (uint32_t)(n0 + nb * 8)) * 2u
+                      ? ((uint32_t)(kb * KB) * (uint32_t)p.ldb +
+                         (uint32_t)(n0 + nb * 8)) * 2u
                       : kOob;
     }
 
     u32x4 ra_reg[NA];
     u32x4 rb_reg[NBB][KB];
 
-    auto gload = [&](int kt) {
+    auto gload_a = [&](int kt) {
       const int k0 = kt * BK;
-      const bool kedge = k0 + BK > p.K; // only the last k-tile of a ragged K
-      const bool a_ok = !kedge || (k0 + a_kc) < p.K;
+      const bool kt_ok = kt < kt_end && (k0 + a_c * 8) < p.K;
 #pragma unroll
       for (int i = 0; i < NA; ++i)
-        ra_reg[i] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       ra, a_ok ? a_voff[i] : kOob, k0 * 2, 0));
+        ra_reg[i] = buf_load16(ra, (kt_ok && i * RS < a_rows_left) ? a_voff : kOob,
+                               k0 * 2 + i * a_soff_step);
+    };
+    auto gload_b = [&](int kt) {
+      const int k0 = kt * BK;
 #pragma unroll
       for (int j = 0; j < NBB; ++j)
 #pragma unroll
         for (int r = 0; r < KB; ++r) {
-          const bool ok = !kedge || (k0 + b_k[j] + r) < p.K;
-          rb_reg[j][r] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         rb, ok ? b_voff[j] : kOob, (k0 + r) * p.ldb * 2, 0));
+          const bool ok = kt < kt_end && (k0 + b_k[j] + r) < p.K;
+          rb_reg[j][r] = buf_load16(rb, ok ? b_voff[j] : kOob, (k0 + r) * p.ldb * 2);
         }
     };
-
-    auto lds_store = [&](int stage) {
+    auto lds_store_a = [&](int stage) {
       u32x4 *As = lds + stage * T::STAGE;
-      u32x4 *Bs = As + T::A_STAGE;
 #pragma unroll
       for (int i = 0; i < NA; ++i) {
-        const int q = tid + i * NT;
-        const int row = q / KCH, c = q % KCH;
-        As[row * KCH + swz<KCH>(row, c)] = ra_reg[i];
+        const int row = a_row0 + i * RS;
+        As[row * KCH + swz<KCH>(row, a_c)] = ra_reg[i];
       }
+    };
+    auto lds_store_b = [&](int stage) {
+      u32x4 *Bs = lds + stage * T::STAGE + T::A_STAGE;
 #pragma unroll
       for (int j = 0; j < NBB; ++j) {
         const int b = tid + j * NT;
@@ -204,7 +236,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const int n = nb * 8 + t;
-          const int dw = t >> 1;      // dword holding column t in each row
+          const int dw = t >> 1; // dword holding column t in each row
           const bool hi = (t & 1) != 0;
           char *rowp = reinterpret_cast<char *>(Bs + n * KCH + swz<KCH>(n, c)) +
                        within * 2;
@@ -238,48 +270,90 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       }
     };
 
-    // ---- main loop: 2 LDS stages + one k-tile of register prefetch -------
-    gload(kt0);
-    lds_store(0);
-    if (nk > 1)
-      gload(kt0 + 1);
+    half8 fa[2][TM], fb[2][TN];
+    auto read_frags = [&](int buf, int stage, int ks) {
+      const u32x4 *As = lds + stage * T::STAGE;
+      const u32x4 *Bs = As + T::A_STAGE;
+      const int c = ks * 2 + khalf;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = fr_a + i * 32;
+        fa[buf][i] = __builtin_bit_cast(half8, As[row * KCH + swz<KCH>(row, c)]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = fr_b + j * 32;
+        fb[buf][j] = __builtin_bit_cast(half8, Bs[row * KCH + swz<KCH>(row, c)]);
+      }
+    };
+    // C^T tile += B^T-fragment x A-fragment, i.e. C += A*B for this k step
+    auto mfma_range = [&](int buf, int lo, int hi) {
+#pragma unroll
+      for (int q = 0; q < NMFMA; ++q) {
+        if (q >= lo && q < hi) {
+          const int i = q / TN, j = q % TN;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i],
+                                                             acc[i][j], 0, 0, 0);
+        }
+      }
+    };
+
+    // ---- prologue: tile kt0 -> LDS stage 0, tile kt0+1 -> registers -------
+    if (persistent)
+      __syncthreads(); // the previous tile's last fragment reads are done
+    gload_a(kt0);
+    gload_b(kt0);
+    lds_store_a(0);
+    lds_store_b(0);
+    gload_a(kt0 + 1);
+    gload_b(kt0 + 1);
     __syncthreads();
+    read_frags(0, 0, 0);
 
-    const int a_row0 = wm * T::WTM + (lane & 31);
-    const int b_row0 = wn * T::WTN + (lane & 31);
-    const int khalf = lane >> 5;
-
+    // ---- main loop --------------------------------------------------------
+    // k-tile `it` is consumed from LDS stage it&1 while tile it+1 moves from
+    // registers into the other stage and tile it+2 is requested from global
+    // memory. Fragments are double-buffered across the 16-deep k steps. The
+    // single barrier per k-tile sits in the middle of the last k step, after
+    // the next stage is complete and before its first fragments are read.
+    // Every step is unconditional (out-of-range tiles load zeros), so one
+    // iteration is one basic block the scheduler can interleave freely.
     for (int it = 0; it < nk; ++it) {
       const int s = it & 1;
-      if (it + 1 < nk) {
-        lds_store(s ^ 1);
-        if (it + 2 < nk)
-          gload(kt0 + it + 2);
-      }
-      const u32x4 *As = lds + s * T::STAGE;
-      const u32x4 *Bs = As + T::A_STAGE;
 #pragma unroll
-      for (int ks = 0; ks < T::KSTEPS; ++ks) {
-        const int c = ks * 2 + khalf;
-        half8 af[TM], bf[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int row = a_row0 + i * 32;
-          af[i] = __builtin_bit_cast(half8, As[row * KCH + swz<KCH>(row, c)]);
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int cur = ks & 1;
+        if (ks + 1 < KSTEPS) {
+          read_frags(cur ^ 1, s, ks + 1);
+          if (ks == T::STEP_A) {
+            lds_store_a(s ^ 1);
+            gload_a(kt0 + it + 2);
+          }
+          if (ks == T::STEP_B) {
+            lds_store_b(s ^ 1);
+            gload_b(kt0 + it + 2);
+          }
+          mfma_range(cur, 0, NMFMA);
+          constexpr int NW = (T::STEP_A == T::STEP_B) ? NA + NBB * 8 : NA;
+          if (ks == T::STEP_A && T::STEP_A == T::STEP_B)
+            sched_step<NMFMA, TM + TN, NA + NBB * 8, NA + NBB * KB>();
+          else if (ks == T::STEP_A)
+            sched_step<NMFMA, TM + TN, NW, NA>();
+          else if (ks == T::STEP_B)
+            sched_step<NMFMA, TM + TN, NBB * 8, NBB * KB>();
+          else
+            sched_step<NMFMA, TM + TN, 0, 0>();
+          __builtin_amdgcn_sched_barrier(0); // k steps do not mix
+        } else {
+          mfma_range(cur, 0, NMFMA / 2);
+          __builtin_amdgcn_sched_barrier(0);
+          __syncthreads();
+          read_frags(cur ^ 1, s ^ 1, 0);
+          mfma_range(cur, NMFMA / 2, NMFMA);
+          sched_step<NMFMA - NMFMA / 2, TM + TN, 0, 0>();
+          __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int row = b_row0 + j * 32;
-          bf[j] = __builtin_bit_cast(half8, Bs[row * KCH + swz<KCH>(row, c)]);
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i],
-                                                               acc[i][j], 0, 0, 0);
       }
-      __syncthreads();
     }
 
     // ---- epilogue ---------------------------------------------------------
@@ -299,7 +373,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             const int col = ccol_base + j * 32 + 8 * g;
             const bool ok = row < p.M && col < p.N;
-            const uint32_t off = ok ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u : kOob;
+            const uint32_t off =
+                ok ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u : kOob;
             const _Float16 h0 = (_Float16)acc[i][j][4 * g + 0];
             const _Float16 h1 = (_Float16)acc[i][j][4 * g + 1];
             const _Float16 h2 = (_Float16)acc[i][j][4 * g + 2];
@@ -328,7 +403,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             const int col = ccol_base + j * 32 + 8 * g;
             const bool ok = row < p.M && col < p.N;
-            const uint32_t off = ok ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u : kOob;
+            const uint32_t off =
+                ok ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u : kOob;
             f32x4 v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
                        acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
             if constexpr (OUT == kOutF32Accum) {
