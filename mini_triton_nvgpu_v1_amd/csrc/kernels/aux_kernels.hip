@@ -173,7 +173,8 @@ const KernelEntry *find_kernel(const KernelKey &k) {
   for (int i = 0; i < n; ++i) {
     const KernelEntry *e = kernel_at(i);
     if (e->key.bm == k.bm && e->key.bn == k.bn && e->key.bk == k.bk &&
-        e->key.wgm == k.wgm && e->key.wgn == k.wgn && e->key.out == k.out)
+        e->key.wgm == k.wgm && e->key.wgn == k.wgn && e->key.out == k.out &&
+        e->key.stages == k.stages)
       return e;
   }
   return nullptr;

@@ -5,14 +5,16 @@
 // IO (lib/Transforms/LowerEpilogueVectorIO.cpp:22-385) with hand-written HIP
 // for wave64 + MFMA + LDS:
 //
-//  * transport: raw buffer_load_dwordx4 (16 B per lane) from row-major A/B,
-//    bounds handled by the buffer descriptor (an out-of-range offset returns
-//    zero), staged in registers one k-tile ahead;
-//  * LDS: two stages of A[BM][BK] and B^T[BN][BK], both K-contiguous so every
-//    MFMA operand is one ds_read_b128; 16-byte chunks XOR-swizzled by
-//    phase(row) = ((row / per_phase) ^ (row / (8 * per_phase))) % max_phase,
-//    per_phase = max(1, 128 / row_bytes), max_phase = row_bytes / 16;
-//    B is transposed in registers (8x8 blocks of f16, v_perm) on its way in;
+//  * transport: buffer_load_dwordx4 ... lds (direct-to-LDS, 16 B per lane,
+//    no register staging) from row-major A/B; bounds handled by the buffer
+//    descriptor (an out-of-range offset loads zero); STAGES-deep ring of LDS
+//    stages, tile it+STAGES-1 in flight while tile it is consumed;
+//  * LDS layouts: A as [BM][BK] (K-contiguous, MFMA operand = one
+//    ds_read_b128), B as [BK][BN] exactly as it lies in memory (N-contiguous,
+//    MFMA operand = two ds_read_b64_tr_b16, the gfx950 transposing read);
+//    16-byte chunks XOR-swizzled so both reads are bank-conflict free:
+//    A chunk ^= (row / per_phase) % max_phase (per_phase = max(1, 128 /
+//    row_bytes), max_phase = row_bytes / 16), B chunk ^= 2 * (k % 4);
 //  * compute: v_mfma_f32_32x32x16_f16 with the B fragment as srcA and the A
 //    fragment as srcB, so each lane's 16 accumulators are 4 runs of 4
 //    consecutive C columns of one row (4 x 8-byte f16 stores per tile);
@@ -59,7 +61,7 @@ struct GemmParams {
 };
 
 struct KernelKey {
-  int bm, bn, bk, wgm, wgn, out;
+  int bm, bn, bk, wgm, wgn, out, stages;
 };
 
 struct KernelEntry {

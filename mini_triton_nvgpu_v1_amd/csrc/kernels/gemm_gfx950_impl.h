@@ -6,11 +6,15 @@
 
 namespace tbk {
 
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef short short4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define TBK_LDS __attribute__((address_space(3)))
 
 // Buffer descriptor dword3 for gfx9-family raw buffers (stride 0, untyped,
 // bounds checked against num_records).
@@ -23,7 +27,6 @@ static constexpr uint32_t kOob = 0x80000000u;
 static constexpr int kSchedMfma = 0x008;
 static constexpr int kSchedVmemRead = 0x020;
 static constexpr int kSchedDsRead = 0x100;
-static constexpr int kSchedDsWrite = 0x200;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p,
                                                             uint32_t bytes) {
@@ -31,19 +34,36 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *p,
                                            (int)bytes, kBufferFlags);
 }
 
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r,
-                                            uint32_t voff, int soff) {
-  return __builtin_bit_cast(
-      u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+// 16 bytes per lane from global memory straight into LDS at
+// lds_base + 16 * lane (lds_base is wave-uniform), i.e.
+// buffer_load_dwordx4 ... offen lds with M0 = lds_base.
+// Issued as inline asm on purpose: the compiler then does not treat it as an
+// LDS write, so it does not put vmcnt(0) in front of every later LDS read
+// (it cannot tell that those reads hit a different stage). Ordering is the
+// kernel's job: wait_vmcnt<N>() + barrier before a stage is read.
+__device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t lds_base,
+                                           uint32_t voff, int soff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_base);
+  const int so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %0\n\t"
+               "buffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "memory");
 }
 
-// Physical 16-byte chunk of (row, chunk) in a K-contiguous LDS tile with
-// KCH chunks per row.
-template <int KCH>
-__device__ __forceinline__ int swz(int row, int chunk) {
-  constexpr int PP = KCH >= 8 ? 1 : 8 / KCH; // rows per phase
-  const int phase = ((row / PP) ^ (row / (8 * PP))) & (KCH - 1);
-  return chunk ^ phase;
+// Raw buffer descriptor as four dwords for inline asm operands.
+__device__ __forceinline__ u32x4 rsrc_dwords(const void *p, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return (u32x4){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes,
+                 (uint32_t)kBufferFlags};
+}
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt untouched), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 // Program id -> (tile_m, tile_n, split part).
@@ -73,74 +93,68 @@ __device__ __forceinline__ void map_program(const GemmParams &p, int pid,
   part = 0;
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OUT>
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES>
 struct GemmTile {
-  static constexpr int NT = WGM * WGN * 64;
+  static constexpr int NW = WGM * WGN; // waves
+  static constexpr int NT = NW * 64;
   static constexpr int WTM = BM / WGM;
   static constexpr int WTN = BN / WGN;
   static constexpr int TM = WTM / 32;
   static constexpr int TN = WTN / 32;
   static constexpr int NMFMA = TM * TN; // MFMAs per 16-deep k step per wave
-  static constexpr int KCH = BK / 8;    // 16-byte chunks per LDS row
   static constexpr int KSTEPS = BK / 16;
-  // A: BM*KCH chunks; thread t owns rows t/KCH + i*RS, chunk t%KCH
-  static constexpr int NA = BM * KCH / NT;
-  static constexpr int RS = NT / KCH;
-  // B: blocks of KB rows x 8 columns, transposed in registers
-  static constexpr int KB = ((BK / 8) * (BN / 8) >= NT)   ? 8
-                            : ((BK / 4) * (BN / 8) >= NT) ? 4
-                            : ((BK / 2) * (BN / 8) >= NT) ? 2
-                                                          : 1;
-  static constexpr int NBB = (BK / KB) * (BN / 8) / NT;
-  static constexpr int A_STAGE = BM * KCH; // in 16-byte chunks
-  static constexpr int B_STAGE = BN * KCH;
+  static constexpr int KCH = BK / 8;  // 16-byte chunks per A row
+  static constexpr int BNC = BN / 8;  // 16-byte chunks per B row
+  static constexpr int A_PP = KCH >= 8 ? 1 : 8 / KCH; // A rows per swizzle phase
+  static constexpr int A_STAGE = BM * KCH;  // 16-byte chunks
+  static constexpr int B_STAGE = BK * BNC;
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LDS_BYTES = 2 * STAGE * 16;
-  // k step (within a k-tile) at which the next tile's A / B are written to
-  // LDS and the tile after that is requested from global memory
-  static constexpr int STEP_A = 0;
-  static constexpr int STEP_B = KSTEPS >= 4 ? 1 : 0;
+  static constexpr int LDS_BYTES = STAGES * STAGE * 16;
+  // direct loads per thread per k-tile
+  static constexpr int LA = A_STAGE / NT;
+  static constexpr int LB = B_STAGE / NT;
+  static constexpr int LPT = LA + LB;
+  static constexpr int A_ROWS_PER_LOAD = NT / KCH; // rows one load round covers
+  static constexpr int B_ROWS_PER_LOAD = NT / BNC;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
-  static_assert(NT % KCH == 0, "threads per A row chunk");
-  static_assert(NA >= 1 && NA * NT == BM * KCH, "A chunks per thread");
-  static_assert(NBB >= 1 && NBB * NT == (BK / KB) * (BN / 8), "B blocks");
+  static_assert(BNC >= 8 && 64 % BNC == 0, "B rows of 64..512 halves");
+  static_assert(LA >= 1 && LA * NT == A_STAGE, "A loads per thread");
+  static_assert(LB >= 1 && LB * NT == B_STAGE, "B loads per thread");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
+  static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
+  static_assert(LPT * (STAGES - 2) < 64, "vmcnt range");
 };
 
-// Interleave one k step's MFMAs with its memory traffic so the matrix pipe
-// never waits behind a burst of LDS or global instructions.
-template <int NMFMA, int NREAD, int NWRITE, int NVMEM>
+template <int NMFMA, int NREAD, int NVMEM>
 __device__ __forceinline__ void sched_step() {
 #pragma unroll
   for (int i = 0; i < NMFMA; ++i) {
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     if (i < NREAD)
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-    if (i < NWRITE)
-      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
     if (i < NVMEM)
       __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
   }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OUT>
+template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int STAGES>
 __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
-  using T = GemmTile<BM, BN, BK, WGM, WGN, OUT>;
-  constexpr int NT = T::NT, KCH = T::KCH, NA = T::NA, KB = T::KB,
-                NBB = T::NBB, TM = T::TM, TN = T::TN, RS = T::RS,
-                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA;
-  __shared__ u32x4 lds[2 * T::STAGE];
+  using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES>;
+  constexpr int NT = T::NT, NW = T::NW, KCH = T::KCH, BNC = T::BNC,
+                TM = T::TM, TN = T::TN, KSTEPS = T::KSTEPS, NMFMA = T::NMFMA,
+                LA = T::LA, LB = T::LB, LPT = T::LPT;
+  __shared__ u32x4 lds[STAGES * T::STAGE];
+  auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
 
-  const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
-  const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
+  const u32x4 ra4 = rsrc_dwords(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
+  const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
 
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
@@ -149,12 +163,27 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   if (p.xcds > 1 && (nprog % p.xcds) == 0)
     prog = (prog % p.xcds) * (nprog / p.xcds) + prog / p.xcds;
 
-  // per-thread constants of the global -> LDS transport
-  const int a_row0 = tid / KCH, a_c = tid % KCH;
-  const int a_soff_step = RS * p.lda * 2; // bytes between this thread's A rows
-  const int fr_a = wm * T::WTM + (lane & 31); // fragment rows in the A tile
-  const int fr_b = wn * T::WTN + (lane & 31); // fragment rows in the B^T tile
+  // ---- direct-load geometry (per thread, fixed for the whole kernel) -----
+  // Load round i of wave w writes LDS chunks (i*NW + w)*64 + lane of a stage.
+  // A: chunk q -> row q / KCH, physical chunk q % KCH holding logical k chunk
+  //    (q % KCH) ^ phase(row); every round keeps the same phase for a lane.
+  const int a_row0 = (wave * 64 + lane) / KCH;
+  const int a_pc = lane % KCH;
+  const int a_lc = a_pc ^ ((a_row0 / T::A_PP) % KCH);
+  // B: chunk q -> k row q / BNC, physical chunk q % BNC holding logical n
+  //    chunk (q % BNC) ^ (2 * (row % 4)); row % 4 is also fixed per lane.
+  const int b_row0 = (wave * 64 + lane) / BNC;
+  const int b_pc = lane % BNC;
+  const int b_lc = b_pc ^ (2 * (b_row0 % 4));
+
+  // ---- fragment-read geometry --------------------------------------------
+  const int fr_a = wm * T::WTM + (lane & 31); // A rows of this lane's srcB
   const int khalf = lane >> 5;
+  // ds_read_b64_tr_b16 lane roles for the B fragment (srcA of the MFMA):
+  // lane l reads 8 bytes at k row 8*(l/32) + (l%16)/4 (+4 for the second
+  // read), n column 16*((l/16)%2) + 4*(l%4) of its 32-column tile.
+  const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_n = wn * T::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   for (int work = prog; work < p.total_work;
        work += (persistent ? nprog : p.total_work)) {
@@ -177,113 +206,66 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = (f32x16){};
 
-    // The k-dependent part of every global address is wave-uniform and rides
-    // in the buffer instruction's scalar offset. A row, column or k-tile
-    // outside the problem gets the vector offset kOob: the load returns 0.
+    // The k-dependent part of each global address is wave-uniform and rides
+    // in the scalar offset; a row, column or k range outside the problem gets
+    // the vector offset kOob, which loads zero.
     const uint32_t a_voff =
-        ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + (uint32_t)(a_c * 8)) * 2u;
-    const int a_rows_left = p.M - m0 - a_row0; // row i valid iff i*RS < left
-    uint32_t b_voff[NBB];
-    int b_k[NBB];
-#pragma unroll
-    for (int j = 0; j < NBB; ++j) {
-      const int b = tid + j * NT;
-      const int kb = b / (BN / 8), nb = b % (BN / 8);
-      b_k[j] = kb * KB;
-      b_voff[j] = (n0 + nb * 8) < p.N
-                      ? ((uint32_t)(kb * KB) * (uint32_t)p.ldb +
-                         (uint32_t)(n0 + nb * 8)) * 2u
-                      : kOob;
-    }
+        ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + (uint32_t)(a_lc * 8)) * 2u;
+    const int a_rows_left = p.M - m0 - a_row0; // round i valid iff i*rows < left
+    const uint32_t b_voff = (n0 + b_lc * 8) < p.N
+                                ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
+                                   (uint32_t)(n0 + b_lc * 8)) * 2u
+                                : kOob;
 
-    u32x4 ra_reg[NA];
-    u32x4 rb_reg[NBB][KB];
-
-    auto gload_a = [&](int kt) {
+    // Issue the direct loads of k-tile kt into LDS stage `stage`.
+    auto issue_tile = [&](int kt, int stage) {
       const int k0 = kt * BK;
-      const bool kt_ok = kt < kt_end && (k0 + a_c * 8) < p.K;
+      const bool kt_ok = kt < kt_end;
+      // LDS byte address of this wave's first 1 KiB block in the stage
+      const uint32_t a_lds =
+          (uint32_t)(uintptr_t)(TBK_LDS void *)stage_base(stage) + wave * 1024u;
+      const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
+      const bool a_kok = kt_ok && (k0 + a_lc * 8) < p.K;
 #pragma unroll
-      for (int i = 0; i < NA; ++i)
-        ra_reg[i] = buf_load16(ra, (kt_ok && i * RS < a_rows_left) ? a_voff : kOob,
-                               k0 * 2 + i * a_soff_step);
-    };
-    auto gload_b = [&](int kt) {
-      const int k0 = kt * BK;
+      for (int i = 0; i < LA; ++i)
+        load_lds16(ra4, a_lds + i * NW * 1024u,
+                   (a_kok && i * T::A_ROWS_PER_LOAD < a_rows_left) ? a_voff : kOob,
+                   k0 * 2 + i * T::A_ROWS_PER_LOAD * p.lda * 2);
 #pragma unroll
-      for (int j = 0; j < NBB; ++j)
-#pragma unroll
-        for (int r = 0; r < KB; ++r) {
-          const bool ok = kt < kt_end && (k0 + b_k[j] + r) < p.K;
-          rb_reg[j][r] = buf_load16(rb, ok ? b_voff[j] : kOob, (k0 + r) * p.ldb * 2);
-        }
-    };
-    auto lds_store_a = [&](int stage) {
-      u32x4 *As = lds + stage * T::STAGE;
-#pragma unroll
-      for (int i = 0; i < NA; ++i) {
-        const int row = a_row0 + i * RS;
-        As[row * KCH + swz<KCH>(row, a_c)] = ra_reg[i];
-      }
-    };
-    auto lds_store_b = [&](int stage) {
-      u32x4 *Bs = lds + stage * T::STAGE + T::A_STAGE;
-#pragma unroll
-      for (int j = 0; j < NBB; ++j) {
-        const int b = tid + j * NT;
-        const int kb = b / (BN / 8), nb = b % (BN / 8);
-        const int kk = kb * KB; // first k of the block inside the tile
-        const int c = kk / 8, within = kk % 8;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int n = nb * 8 + t;
-          const int dw = t >> 1; // dword holding column t in each row
-          const bool hi = (t & 1) != 0;
-          char *rowp = reinterpret_cast<char *>(Bs + n * KCH + swz<KCH>(n, c)) +
-                       within * 2;
-          if constexpr (KB == 8) {
-            u32x4 v;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t lo = rb_reg[j][2 * q][dw], up = rb_reg[j][2 * q + 1][dw];
-              v[q] = hi ? ((lo >> 16) | (up & 0xffff0000u))
-                        : ((lo & 0xffffu) | (up << 16));
-            }
-            *reinterpret_cast<u32x4 *>(rowp) = v;
-          } else if constexpr (KB == 4) {
-            u32x2 v;
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const uint32_t lo = rb_reg[j][2 * q][dw], up = rb_reg[j][2 * q + 1][dw];
-              v[q] = hi ? ((lo >> 16) | (up & 0xffff0000u))
-                        : ((lo & 0xffffu) | (up << 16));
-            }
-            *reinterpret_cast<u32x2 *>(rowp) = v;
-          } else if constexpr (KB == 2) {
-            const uint32_t lo = rb_reg[j][0][dw], up = rb_reg[j][1][dw];
-            *reinterpret_cast<uint32_t *>(rowp) =
-                hi ? ((lo >> 16) | (up & 0xffff0000u)) : ((lo & 0xffffu) | (up << 16));
-          } else {
-            const uint32_t w = rb_reg[j][0][dw];
-            *reinterpret_cast<uint16_t *>(rowp) = (uint16_t)(hi ? (w >> 16) : w);
-          }
-        }
+      for (int i = 0; i < LB; ++i) {
+        const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
+        load_lds16(rb4, b_lds + i * NW * 1024u,
+                   (kt_ok && krow < p.K) ? b_voff : kOob,
+                   (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
       }
     };
 
     half8 fa[2][TM], fb[2][TN];
     auto read_frags = [&](int buf, int stage, int ks) {
-      const u32x4 *As = lds + stage * T::STAGE;
-      const u32x4 *Bs = As + T::A_STAGE;
+      const TBK_LDS u32x4 *As = (const TBK_LDS u32x4 *)stage_base(stage);
+      const TBK_LDS char *Bs = (const TBK_LDS char *)(As + T::A_STAGE);
       const int c = ks * 2 + khalf;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = fr_a + i * 32;
-        fa[buf][i] = __builtin_bit_cast(half8, As[row * KCH + swz<KCH>(row, c)]);
+        fa[buf][i] = __builtin_bit_cast(
+            half8, As[row * KCH + (c ^ ((row / T::A_PP) % KCH))]);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int row = fr_b + j * 32;
-        fb[buf][j] = __builtin_bit_cast(half8, Bs[row * KCH + swz<KCH>(row, c)]);
+        const int n = tr_n + j * 32;
+        half4 h[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = ks * 16 + tr_k + 4 * r;
+          const int pc = (n >> 3) ^ (2 * (k & 3));
+          const TBK_LDS short4 *src = (const TBK_LDS short4 *)(
+              Bs + k * (BN * 2) + pc * 16 + (n & 7) * 2);
+          h[r] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                               (TBK_LDS short4 *)src));
+        }
+        fb[buf][j] = (half8){h[0][0], h[0][1], h[0][2], h[0][3],
+                             h[1][0], h[1][1], h[1][2], h[1][3]};
       }
     };
     // C^T tile += B^T-fragment x A-fragment, i.e. C += A*B for this k step
@@ -298,62 +280,53 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       }
     };
 
-    // ---- prologue: tile kt0 -> LDS stage 0, tile kt0+1 -> registers -------
+    // ---- prologue: tiles kt0 .. kt0+STAGES-2 in flight -----------------------
     if (persistent)
       __syncthreads(); // the previous tile's last fragment reads are done
-    gload_a(kt0);
-    gload_b(kt0);
-    lds_store_a(0);
-    lds_store_b(0);
-    gload_a(kt0 + 1);
-    gload_b(kt0 + 1);
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+      issue_tile(kt0 + st, st);
+    wait_vmcnt<LPT * (STAGES - 2)>();
     __syncthreads();
     read_frags(0, 0, 0);
 
     // ---- main loop --------------------------------------------------------
-    // k-tile `it` is consumed from LDS stage it&1 while tile it+1 moves from
-    // registers into the other stage and tile it+2 is requested from global
-    // memory. Fragments are double-buffered across the 16-deep k steps. The
-    // single barrier per k-tile sits in the middle of the last k step, after
-    // the next stage is complete and before its first fragments are read.
-    // Every step is unconditional (out-of-range tiles load zeros), so one
+    // Tile `it` is consumed from stage it % STAGES while tiles up to
+    // it+STAGES-1 stream into the other stages. Fragments are double-buffered
+    // across the 16-deep k steps. The one barrier per k-tile sits in the
+    // middle of the last k step: it publishes tile it+1 (after this wave's
+    // vmcnt shows that tile landed) and frees stage it % STAGES for reuse.
+    // All steps are unconditional (out-of-range tiles load zeros), so an
     // iteration is one basic block the scheduler can interleave freely.
+    int s = 0;
     for (int it = 0; it < nk; ++it) {
-      const int s = it & 1;
+      const int s_next = s + 1 == STAGES ? 0 : s + 1;
+      const int s_fill = s == 0 ? STAGES - 1 : s - 1; // stage freed by it-1
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         const int cur = ks & 1;
         if (ks + 1 < KSTEPS) {
           read_frags(cur ^ 1, s, ks + 1);
-          if (ks == T::STEP_A) {
-            lds_store_a(s ^ 1);
-            gload_a(kt0 + it + 2);
-          }
-          if (ks == T::STEP_B) {
-            lds_store_b(s ^ 1);
-            gload_b(kt0 + it + 2);
-          }
+          if (ks == 0)
+            issue_tile(kt0 + it + STAGES - 1, s_fill);
           mfma_range(cur, 0, NMFMA);
-          constexpr int NW = (T::STEP_A == T::STEP_B) ? NA + NBB * 8 : NA;
-          if (ks == T::STEP_A && T::STEP_A == T::STEP_B)
-            sched_step<NMFMA, TM + TN, NA + NBB * 8, NA + NBB * KB>();
-          else if (ks == T::STEP_A)
-            sched_step<NMFMA, TM + TN, NW, NA>();
-          else if (ks == T::STEP_B)
-            sched_step<NMFMA, TM + TN, NBB * 8, NBB * KB>();
+          if (ks == 0)
+            sched_step<NMFMA, TM + 2 * TN, LPT>();
           else
-            sched_step<NMFMA, TM + TN, 0, 0>();
+            sched_step<NMFMA, TM + 2 * TN, 0>();
           __builtin_amdgcn_sched_barrier(0); // k steps do not mix
         } else {
           mfma_range(cur, 0, NMFMA / 2);
           __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<LPT * (STAGES - 2)>();
           __syncthreads();
-          read_frags(cur ^ 1, s ^ 1, 0);
+          read_frags(cur ^ 1, s_next, 0);
           mfma_range(cur, NMFMA / 2, NMFMA);
-          sched_step<NMFMA - NMFMA / 2, TM + TN, 0, 0>();
+          sched_step<NMFMA - NMFMA / 2, TM + 2 * TN, 0>();
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+      s = s_next;
     }
 
     // ---- epilogue ---------------------------------------------------------
@@ -443,7 +416,13 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 } // namespace tbk
 
 // One registry entry per instance.
-#define TBK_ENTRY(BM, BN, BK, WGM, WGN, OUT)                                     \
-  {{BM, BN, BK, WGM, WGN, OUT},                                                  \
-   reinterpret_cast<const void *>(&tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT>), \
-   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_out" #OUT}
+#define TBK_ENTRY(BM, BN, BK, WGM, WGN, OUT, ST)                                 \
+  {{BM, BN, BK, WGM, WGN, OUT, ST},                                              \
+   reinterpret_cast<const void *>(                                               \
+       &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST>),                        \
+   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT}
+
+#define TBK_OUTS(BM, BN, BK, WGM, WGN, ST)                                      \
+  TBK_ENTRY(BM, BN, BK, WGM, WGN, 0, ST), TBK_ENTRY(BM, BN, BK, WGM, WGN, 1, ST), \
+      TBK_ENTRY(BM, BN, BK, WGM, WGN, 2, ST),                                   \
+      TBK_ENTRY(BM, BN, BK, WGM, WGN, 3, ST)

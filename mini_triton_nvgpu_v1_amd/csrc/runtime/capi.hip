@@ -126,15 +126,17 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
     return fail("too many programs");
 
   tbk::KernelKey key{(int)c.block_m, (int)c.block_n, (int)c.block_k,
-                     (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode};
+                     (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode,
+                     (int)c.stages};
   const tbk::KernelEntry *e = tbk::find_kernel(key);
   if (!e) {
     char buf[256];
     snprintf(buf, sizeof buf,
              "no gfx950 kernel instance for tile %lldx%lldx%lld, wave grid "
-             "%lldx%lld, output mode %d",
+             "%lldx%lld, %lld LDS stages, output mode %d",
              (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
-             (long long)c.wave_grid_m, (long long)c.wave_grid_n, out_mode);
+             (long long)c.wave_grid_m, (long long)c.wave_grid_n,
+             (long long)c.stages, out_mode);
     return fail(buf);
   }
   tb_gemm_desc *d = new tb_gemm_desc();
@@ -146,7 +148,7 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
   d->tiles_n = tiles_n;
   d->tiles_k = tiles_k;
   d->total_work = total_work;
-  d->lds_bytes = 2 * (c.block_m + c.block_n) * c.block_k * 2;
+  d->lds_bytes = c.stages * (c.block_m + c.block_n) * c.block_k * 2;
   d->workspace_bytes = c.reduction == TB_RED_WORKSPACE
                            ? (size_t)(c.split_k * c.m * c.n * 4)
                            : 0;

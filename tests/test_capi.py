@@ -51,7 +51,7 @@ def test_abi_version_and_struct_layout(tmp_path):
 def test_kernel_registry_names():
     names = tb.kernel_names()
     assert len(names) >= 40
-    assert "tb_gemm_gfx950_256x256x64_w2x2_out0" in names
+    assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0" in names
 
 
 @pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
@@ -59,7 +59,7 @@ def test_every_workload_has_an_instance(w):
     d = tb.GemmDesc.from_config(w.direct_config())
     bm, bn, bk = w.block
     assert d.kernel_name.startswith(f"tb_gemm_gfx950_{bm}x{bn}x{bk}_")
-    assert d.lds_bytes == 2 * (bm + bn) * bk * 2
+    assert d.lds_bytes == w.stages * (bm + bn) * bk * 2
     if w.split_k > 1:
         assert d.workspace_bytes == w.split_k * w.M * w.N * 4
     else:

@@ -97,26 +97,27 @@ def test_ragged_edges(M, N, K, tile, device):
 def _every_instance():
     seen = set()
     for name in tb.kernel_names():
-        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_out{OUT}
+        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{STAGES}_out{OUT}
         body = name[len("tb_gemm_gfx950_"):]
-        shape, waves, out = body.split("_")
+        shape, waves, stages, out = body.split("_")
         bm, bn, bk = map(int, shape.split("x"))
         wgm, wgn = map(int, waves[1:].split("x"))
-        seen.add((bm, bn, bk, wgm, wgn, int(out[3:])))
+        seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:])))
     return sorted(seen)
 
 
 @pytest.mark.parametrize("inst", _every_instance(), ids=lambda t: "x".join(map(str, t)))
 def test_every_instance(inst, device):
-    """Each compiled instance on a shape with several K tiles and an M/N edge."""
-    bm, bn, bk, wgm, wgn, out = inst
-    M, N, K = bm + 40, bn * 2 - 24, bk * 5
+    """Each compiled instance on a shape with several K tiles (more than the
+    stage count, plus a ragged last tile when possible) and an M/N edge."""
+    bm, bn, bk, wgm, wgn, stages, out = inst
+    M, N, K = bm + 40, bn * 2 - 24, bk * 5 + (bk // 2 if out == 0 else 0)
     print(f"instance {inst} on {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0200 + bm + bn + bk, oracle.UNIFORM)
     tm, tn = -(-M // bm), -(-N // bn)
     kw = dict(m=M, n=N, k=K, lda=K, ldb=N, ldc=N, block_m=bm, block_n=bn,
               block_k=bk, num_waves=wgm * wgn, wave_grid_m=wgm, wave_grid_n=wgn,
-              stages=2, group_m=8, xcd_remap=0)
+              stages=stages, group_m=8, xcd_remap=0)
     rng = np.random.default_rng(out)
     init = None
     if out == 0:
