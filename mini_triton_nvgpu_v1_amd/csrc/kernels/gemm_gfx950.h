@@ -12,9 +12,10 @@
 //  * LDS layouts: A as [BM][BK] (K-contiguous, MFMA operand = one
 //    ds_read_b128), B as [BK][BN] exactly as it lies in memory (N-contiguous,
 //    MFMA operand = two ds_read_b64_tr_b16, the gfx950 transposing read);
-//    16-byte chunks XOR-swizzled so both reads are bank-conflict free:
-//    A chunk ^= (row / per_phase) % max_phase (per_phase = max(1, 128 /
-//    row_bytes), max_phase = row_bytes / 16), B chunk ^= 2 * (k % 4);
+//    XOR swizzles keep both reads bank-conflict free on the 64-bank
+//    (256 B/cycle) LDS: A 16-byte chunk ^= (row / per_phase) % max_phase
+//    (per_phase = max(1, 256 / row_bytes), max_phase = row_bytes / 16);
+//    B 64-byte segment ^= (k / per_phase) % min(4, segments per row);
 //  * compute: v_mfma_f32_32x32x16_f16 with the B fragment as srcA and the A
 //    fragment as srcB, so each lane's 16 accumulators are 4 runs of 4
 //    consecutive C columns of one row (4 x 8-byte f16 stores per tile);

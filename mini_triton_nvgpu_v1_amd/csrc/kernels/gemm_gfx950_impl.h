@@ -105,7 +105,16 @@ struct GemmTile {
   static constexpr int KSTEPS = BK / 16;
   static constexpr int KCH = BK / 8;  // 16-byte chunks per A row
   static constexpr int BNC = BN / 8;  // 16-byte chunks per B row
-  static constexpr int A_PP = KCH >= 8 ? 1 : 8 / KCH; // A rows per swizzle phase
+  // LDS swizzles, both of the form chunk' = chunk ^ ((row / PP) % MAXPH)
+  // with the bank period of gfx950 LDS (64 banks x 4 B = 256 B per cycle:
+  // 16 lanes of ds_read_b128 or 32 lanes of ds_read_b64_tr_b16 at a time).
+  // A: 16-byte chunks, PP = rows per 256 B, MAXPH = chunks per row.
+  static constexpr int A_PP = 256 / (BK * 2) >= 1 ? 256 / (BK * 2) : 1;
+  // B: 64-byte segments (the 32 columns two 16-lane tr groups read per row),
+  // PP = rows per 256 B, MAXPH = min(4, segments per row); in 16-byte chunks
+  // the XOR value is 4 * phase.
+  static constexpr int B_PP = 256 / (BN * 2) >= 1 ? 256 / (BN * 2) : 1;
+  static constexpr int B_MAXPH = BNC / 4 < 4 ? BNC / 4 : 4;
   static constexpr int A_STAGE = BM * KCH;  // 16-byte chunks
   static constexpr int B_STAGE = BK * BNC;
   static constexpr int STAGE = A_STAGE + B_STAGE;
@@ -114,17 +123,26 @@ struct GemmTile {
   static constexpr int LA = A_STAGE / NT;
   static constexpr int LB = B_STAGE / NT;
   static constexpr int LPT = LA + LB;
+  // vmcnt allowed at the prologue wait / the per-tile barrier = loads issued
+  // after the tile being waited for (vmcnt retires in issue order): the
+  // prologue fills all STAGES stages; the loop waits for tile it+1 while
+  // tiles it+2 .. it+STAGES-1 may still be in flight.
+  static constexpr int VM_PROLOGUE = (STAGES - 1) * LPT;
+  static constexpr int VM_LOOP = (STAGES - 2) * LPT;
   static constexpr int A_ROWS_PER_LOAD = NT / KCH; // rows one load round covers
   static constexpr int B_ROWS_PER_LOAD = NT / BNC;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
   static_assert(BNC >= 8 && 64 % BNC == 0, "B rows of 64..512 halves");
+  static_assert(B_ROWS_PER_LOAD % B_PP == 0 &&
+                    (B_ROWS_PER_LOAD / B_PP) % B_MAXPH == 0,
+                "a lane's B swizzle phase is the same in every load round");
   static_assert(LA >= 1 && LA * NT == A_STAGE, "A loads per thread");
   static_assert(LB >= 1 && LB * NT == B_STAGE, "B loads per thread");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
-  static_assert(LPT * (STAGES - 2) < 64, "vmcnt range");
+  static_assert(VM_LOOP < 64 && VM_PROLOGUE < 64, "vmcnt range");
 };
 
 template <int NMFMA, int NREAD, int NVMEM>
@@ -166,15 +184,18 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   // ---- direct-load geometry (per thread, fixed for the whole kernel) -----
   // Load round i of wave w writes LDS chunks (i*NW + w)*64 + lane of a stage.
   // A: chunk q -> row q / KCH, physical chunk q % KCH holding logical k chunk
-  //    (q % KCH) ^ phase(row); every round keeps the same phase for a lane.
+  //    (q % KCH) ^ ((row / A_PP) % KCH); the row advances by A_ROWS_PER_LOAD
+  //    per round, so the logical chunk is recomputed per round.
   const int a_row0 = (wave * 64 + lane) / KCH;
   const int a_pc = lane % KCH;
-  const int a_lc = a_pc ^ ((a_row0 / T::A_PP) % KCH);
+  auto a_lchunk = [&](int i) {
+    return a_pc ^ (((a_row0 + i * T::A_ROWS_PER_LOAD) / T::A_PP) % KCH);
+  };
   // B: chunk q -> k row q / BNC, physical chunk q % BNC holding logical n
-  //    chunk (q % BNC) ^ (2 * (row % 4)); row % 4 is also fixed per lane.
+  //    chunk (q % BNC) ^ (4 * ((row / B_PP) % B_MAXPH)), fixed per lane.
   const int b_row0 = (wave * 64 + lane) / BNC;
   const int b_pc = lane % BNC;
-  const int b_lc = b_pc ^ (2 * (b_row0 % 4));
+  const int b_lc = b_pc ^ (4 * ((b_row0 / T::B_PP) % T::B_MAXPH));
 
   // ---- fragment-read geometry --------------------------------------------
   const int fr_a = wm * T::WTM + (lane & 31); // A rows of this lane's srcB
@@ -209,8 +230,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // The k-dependent part of each global address is wave-uniform and rides
     // in the scalar offset; a row, column or k range outside the problem gets
     // the vector offset kOob, which loads zero.
-    const uint32_t a_voff =
-        ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + (uint32_t)(a_lc * 8)) * 2u;
+    const uint32_t a_vrow = (uint32_t)(m0 + a_row0) * (uint32_t)p.lda * 2u;
     const int a_rows_left = p.M - m0 - a_row0; // round i valid iff i*rows < left
     const uint32_t b_voff = (n0 + b_lc * 8) < p.N
                                 ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
@@ -225,12 +245,13 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       const uint32_t a_lds =
           (uint32_t)(uintptr_t)(TBK_LDS void *)stage_base(stage) + wave * 1024u;
       const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
-      const bool a_kok = kt_ok && (k0 + a_lc * 8) < p.K;
 #pragma unroll
-      for (int i = 0; i < LA; ++i)
-        load_lds16(ra4, a_lds + i * NW * 1024u,
-                   (a_kok && i * T::A_ROWS_PER_LOAD < a_rows_left) ? a_voff : kOob,
+      for (int i = 0; i < LA; ++i) {
+        const int lc = a_lchunk(i);
+        const bool ok = kt_ok && (k0 + lc * 8) < p.K && i * T::A_ROWS_PER_LOAD < a_rows_left;
+        load_lds16(ra4, a_lds + i * NW * 1024u, ok ? a_vrow + lc * 16u : kOob,
                    k0 * 2 + i * T::A_ROWS_PER_LOAD * p.lda * 2);
+      }
 #pragma unroll
       for (int i = 0; i < LB; ++i) {
         const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
@@ -258,7 +279,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int k = ks * 16 + tr_k + 4 * r;
-          const int pc = (n >> 3) ^ (2 * (k & 3));
+          const int pc = (n >> 3) ^ (4 * ((k / T::B_PP) % T::B_MAXPH));
           const TBK_LDS short4 *src = (const TBK_LDS short4 *)(
               Bs + k * (BN * 2) + pc * 16 + (n & 7) * 2);
           h[r] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -280,47 +301,46 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       }
     };
 
-    // ---- prologue: tiles kt0 .. kt0+STAGES-2 in flight -----------------------
+    // ---- prologue: tiles kt0 .. kt0+STAGES-1 in flight, one per stage ------
     if (persistent)
       __syncthreads(); // the previous tile's last fragment reads are done
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
+    for (int st = 0; st < STAGES; ++st)
       issue_tile(kt0 + st, st);
-    wait_vmcnt<LPT * (STAGES - 2)>();
+    wait_vmcnt<T::VM_PROLOGUE>();
     __syncthreads();
     read_frags(0, 0, 0);
 
     // ---- main loop --------------------------------------------------------
-    // Tile `it` is consumed from stage it % STAGES while tiles up to
-    // it+STAGES-1 stream into the other stages. Fragments are double-buffered
+    // Tile `it` is consumed from stage it % STAGES while the next STAGES-1
+    // tiles stream into the other stages. Fragments are double-buffered
     // across the 16-deep k steps. The one barrier per k-tile sits in the
-    // middle of the last k step: it publishes tile it+1 (after this wave's
-    // vmcnt shows that tile landed) and frees stage it % STAGES for reuse.
-    // All steps are unconditional (out-of-range tiles load zeros), so an
-    // iteration is one basic block the scheduler can interleave freely.
+    // middle of the last k step: after it, tile it+1 (waited for with vmcnt
+    // before the barrier) is visible, and stage it % STAGES is free, so it is
+    // refilled with tile it+STAGES at once. All steps are unconditional
+    // (out-of-range tiles load zeros), so an iteration is one basic block
+    // the scheduler can interleave freely.
     int s = 0;
     for (int it = 0; it < nk; ++it) {
       const int s_next = s + 1 == STAGES ? 0 : s + 1;
-      const int s_fill = s == 0 ? STAGES - 1 : s - 1; // stage freed by it-1
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         const int cur = ks & 1;
         if (ks + 1 < KSTEPS) {
           read_frags(cur ^ 1, s, ks + 1);
-          if (ks == 0)
-            issue_tile(kt0 + it + STAGES - 1, s_fill);
           mfma_range(cur, 0, NMFMA);
           if (ks == 0)
-            sched_step<NMFMA, TM + 2 * TN, LPT>();
+            sched_step<NMFMA, TM + 2 * TN, 0>();
           else
             sched_step<NMFMA, TM + 2 * TN, 0>();
           __builtin_amdgcn_sched_barrier(0); // k steps do not mix
         } else {
           mfma_range(cur, 0, NMFMA / 2);
           __builtin_amdgcn_sched_barrier(0);
-          wait_vmcnt<LPT * (STAGES - 2)>();
+          wait_vmcnt<T::VM_LOOP>();
           __syncthreads();
           read_frags(cur ^ 1, s_next, 0);
+          issue_tile(kt0 + it + STAGES, s);
           mfma_range(cur, NMFMA / 2, NMFMA);
           sched_step<NMFMA - NMFMA / 2, TM + 2 * TN, 0>();
           __builtin_amdgcn_sched_barrier(0);
@@ -328,6 +348,10 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       }
       s = s_next;
     }
+
+    // Drain the (out-of-range, zero) loads still in flight into LDS so none
+    // can land after this tile: the next tile or workgroup reuses the space.
+    wait_vmcnt<0>();
 
     // ---- epilogue ---------------------------------------------------------
     // lane holds C[m0 + wm*WTM + i*32 + lane%32][n0 + wn*WTN + j*32 + 8g + 4h + r]
