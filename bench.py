@@ -38,7 +38,8 @@ def time_workload(w, steps: int, warmup: int, device):
     import torch
     import mini_triton_nvgpu_v1_amd as tb
 
-    desc = tb.GemmDesc.from_config(w.direct_config())
+    # the product path: tb.matmul module text -> plan pipeline -> kernel
+    desc = tb.plan_from_mlir(w.mlir())
     A = torch.empty((w.M, w.K), dtype=torch.float16, device=device)
     B = torch.empty((w.K, w.N), dtype=torch.float16, device=device)
     C = torch.empty((w.M, w.N), dtype=torch.float16, device=device)

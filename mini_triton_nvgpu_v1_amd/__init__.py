@@ -57,6 +57,12 @@ class GemmConfig(ctypes.Structure):
     def as_dict(self) -> dict:
         return {name: getattr(self, name) for name, _ in self._fields_}
 
+    def __eq__(self, other) -> bool:
+        return isinstance(other, GemmConfig) and self.as_dict() == other.as_dict()
+
+    def __repr__(self) -> str:
+        return f"GemmConfig({self.as_dict()})"
+
 
 _lib = None
 

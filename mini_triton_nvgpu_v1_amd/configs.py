@@ -80,7 +80,9 @@ class Workload:
             f"}}\n")
 
     def direct_config(self) -> GemmConfig:
-        """Flattened descriptor equivalent to what the plan pipeline derives."""
+        """Flattened descriptor equal to what the plan pipeline derives
+        (tb_plan_from_mlir on ``self.mlir()``); the tests check the two agree
+        field by field."""
         bm, bn, bk = self.block
         wg = {1: (1, 1), 2: (2, 1), 4: (2, 2), 8: (2, 4)}[self.num_waves]
         tiles_m, tiles_n = -(-self.M // bm), -(-self.N // bn)
@@ -101,10 +103,12 @@ class Workload:
             c_dtype=DTYPE_F16, acc_init=ACC_INIT_ZERO, block_m=bm, block_n=bn,
             block_k=bk, num_waves=self.num_waves, wave_grid_m=wg[0],
             wave_grid_n=wg[1], stages=self.stages, mapping=mapping,
-            group_m=self.group_m if mapping != MAP_TILE else 1,
+            group_m=self.group_m if mapping not in (MAP_TILE, MAP_SPLIT_K) else 1,
             split_k=self.split_k,
             reduction=RED_WORKSPACE if self.split_k > 1 else RED_NONE,
-            num_programs=programs, xcd_remap=8)
+            num_programs=programs,
+            # XCD-aware program order once the tiles outnumber the 256 CUs
+            xcd_remap=8 if tiles_m * tiles_n > 256 else 0)
 
 
 SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,

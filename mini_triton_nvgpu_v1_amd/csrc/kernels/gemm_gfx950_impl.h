@@ -160,9 +160,8 @@ __device__ __forceinline__ void sched_step() {
 template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int STAGES>
 __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES>;
-  constexpr int NT = T::NT, NW = T::NW, KCH = T::KCH, BNC = T::BNC,
-                TM = T::TM, TN = T::TN, KSTEPS = T::KSTEPS, NMFMA = T::NMFMA,
-                LA = T::LA, LB = T::LB, LPT = T::LPT;
+  constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
+                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LB = T::LB;
   __shared__ u32x4 lds[STAGES * T::STAGE];
   auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };
 

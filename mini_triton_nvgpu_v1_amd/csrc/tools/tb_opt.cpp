@@ -1,1 +1,104 @@
-int main(){return 0;}
+// tb-opt: the plan-pipeline driver (reference tools/tb-opt.cpp:11-24, an
+// MlirOptMain over the tb passes). Reads textual IR, runs the passes named
+// by --pass-pipeline or by individual --<pass>[=<options>] flags in command
+// line order, and prints the resulting IR.
+//
+//   tb-opt in.mlir --pass-pipeline='builtin.module(tb-stage1-full-to-gfx950-pipeline{cubin-chip=gfx950})' -o out.mlir
+//   tb-opt in.mlir --tb-verify-scope --tb-attach-target-info='gpu-arch=gfx950'
+//
+// Diagnostics go to stderr as `<file>: error: <message>` with exit code 1.
+#include "../passes/passes.h"
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <sstream>
+
+namespace {
+
+std::string readAll(const std::string &path) {
+  if (path == "-") {
+    std::ostringstream ss;
+    ss << std::cin.rdbuf();
+    return ss.str();
+  }
+  std::ifstream in(path, std::ios::binary);
+  if (!in)
+    throw tb::Error("cannot open `" + path + "`");
+  std::ostringstream ss;
+  ss << in.rdbuf();
+  return ss.str();
+}
+
+void usage() {
+  std::printf("usage: tb-opt [input.mlir|-] [-o output] "
+              "[--pass-pipeline='builtin.module(...)'] [--<pass>[=<options>]]...\n"
+              "       tb-opt --list-passes\n");
+}
+
+} // namespace
+
+int main(int argc, char **argv) {
+  std::string input = "-", output = "-";
+  std::vector<tb::PassSpec> passes;
+  try {
+    for (int i = 1; i < argc; ++i) {
+      std::string a = argv[i];
+      if (a == "-h" || a == "--help") {
+        usage();
+        return 0;
+      }
+      if (a == "--list-passes") {
+        for (const tb::PassInfo &p : tb::registeredPasses())
+          std::printf("%-40s %s\n", p.name.c_str(), p.summary.c_str());
+        return 0;
+      }
+      if (a == "-o") {
+        if (++i >= argc)
+          throw tb::Error("-o needs a path");
+        output = argv[i];
+      } else if (a.rfind("--pass-pipeline=", 0) == 0) {
+        for (tb::PassSpec &p : tb::parsePassPipeline(a.substr(16)))
+          passes.push_back(p);
+      } else if (a == "--pass-pipeline") {
+        if (++i >= argc)
+          throw tb::Error("--pass-pipeline needs a value");
+        for (tb::PassSpec &p : tb::parsePassPipeline(argv[i]))
+          passes.push_back(p);
+      } else if (a.rfind("--tb-", 0) == 0) {
+        std::string body = a.substr(2);
+        size_t eq = body.find('=');
+        std::string spec = eq == std::string::npos
+                               ? body
+                               : body.substr(0, eq) + "{" + body.substr(eq + 1) + "}";
+        for (tb::PassSpec &p : tb::parsePassPipeline(spec))
+          passes.push_back(p);
+      } else if (!a.empty() && a[0] == '-' && a != "-") {
+        throw tb::Error("unknown option `" + a + "`");
+      } else {
+        input = a;
+      }
+    }
+  } catch (const tb::Error &e) {
+    std::fprintf(stderr, "tb-opt: error: %s\n", e.what());
+    return 1;
+  }
+  try {
+    tb::Module m = tb::parseModule(readAll(input));
+    tb::runPipeline(m, passes);
+    std::string text = tb::printModule(m);
+    if (output == "-") {
+      std::fwrite(text.data(), 1, text.size(), stdout);
+    } else {
+      std::ofstream out(output, std::ios::binary);
+      if (!out)
+        throw tb::Error("cannot write `" + output + "`");
+      out << text;
+    }
+  } catch (const tb::Error &e) {
+    std::fprintf(stderr, "%s: error: %s\n", input.c_str(), e.what());
+    return 1;
+  }
+  return 0;
+}

@@ -40,7 +40,7 @@ def main() -> int:
     print(f"profiling: {args.copy_reps} copies of {args.copy_mib} MiB", flush=True)
 
     w = configs.BY_NAME[args.workload]
-    desc = tb.GemmDesc.from_config(w.direct_config())
+    desc = tb.plan_from_mlir(w.mlir())
     A = torch.empty((w.M, w.K), dtype=torch.float16, device=dev)
     B = torch.empty((w.K, w.N), dtype=torch.float16, device=dev)
     C = torch.empty((w.M, w.N), dtype=torch.float16, device=dev)

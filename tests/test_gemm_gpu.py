@@ -53,9 +53,10 @@ def check(got, A16, B16, init=None, rows=None):
                                configs.SPLIT_K, configs.ROOFLINE],
                          ids=lambda w: w.name)
 def test_workload_parity(w, device):
+    """The product path: tb.matmul module text -> plan pipeline -> kernel."""
     print(f"workload {w.name} {w.M}x{w.N}x{w.K}", flush=True)
     A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
-    desc = tb.GemmDesc.from_config(w.direct_config())
+    desc = tb.plan_from_mlir(w.mlir())
     got = run_desc(desc, A, B, device)
     check(got, A, B)
 
@@ -65,10 +66,49 @@ def test_persistent_8192_parity_row_sample(device):
     w = configs.PERSISTENT
     print(f"workload {w.name}", flush=True)
     A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
-    desc = tb.GemmDesc.from_config(w.direct_config())
+    desc = tb.plan_from_mlir(w.mlir())
     got = run_desc(desc, A, B, device)
     assert not np.isnan(got).any()
     check(got, A, B, rows=[(0, 40), (4080, 4128), (8150, 8192)])
+
+
+# Modules of the tb-opt contract tests with an f32 C, which the plan maps to
+# C += A B (the reference's tb.matmul semantics): C starts from a seeded
+# non-zero value and the oracle adds it.
+PLAN_MODULES = [
+    ("exact_f32_1wave", 64, 64, 32, 1, ""),
+    ("grouped_f32", 192, 128, 32, 4, ""),
+    ("ragged_f32_1wave", 96, 80, 32, 1, ""),
+    ("two_wave_f32", 64, 64, 32, 2, ""),
+    ("persistent_grouped_f32", 192, 128, 32, 4,
+     ', "tb.persistent" = true, "tb.num-ctas" = 2 : i64'),
+    ("splitk_atomic_f32", 64, 64, 64, 1,
+     ', "tb.split-k" = 2 : i64, "tb.reduction-mode" = "split_k_parallel"'),
+    ("splitk_serial_f32", 64, 64, 128, 1,
+     ', "tb.split-k" = 3 : i64, "tb.reduction-mode" = "split_k_serial"'),
+]
+
+
+@pytest.mark.parametrize("name,M,N,K,warps,extra", PLAN_MODULES,
+                         ids=[p[0] for p in PLAN_MODULES])
+def test_plan_module_f32_accumulate(name, M, N, K, warps, extra, device):
+    exact = "true" if M % 64 == 0 and N % 64 == 0 else "false"
+    gm = ", group_m = 2 : i64" if name == "grouped_f32" else ""
+    text = (
+        f'module attributes {{"tb.num-warps" = {warps} : i64, '
+        f'"tb.requested-stages" = 2 : i64{extra}}} {{\n'
+        f"  func.func @kernel(%A: memref<{M}x{K}xf16>, %B: memref<{K}x{N}xf16>, "
+        f"%C: memref<{M}x{N}xf32>) {{\n"
+        f"    tb.matmul %A, %B, %C {{block_m = 64 : i64, block_n = 64 : i64, "
+        f"block_k = 32 : i64, exact_tile = {exact}{gm}}} : memref<{M}x{K}xf16>, "
+        f"memref<{K}x{N}xf16>, memref<{M}x{N}xf32>\n    return\n  }}\n}}\n")
+    print(f"plan module {name}", flush=True)
+    desc = tb.plan_from_mlir(text)
+    assert desc.config.acc_init == tb.ACC_INIT_LOAD_C
+    A, B = oracle.config_inputs(M, N, K, 0x5EED0500, oracle.UNIFORM)
+    C0 = oracle.fill_f16(M, N, 0x5EED0501, oracle.UNIFORM, 4.0).astype(np.float32)
+    got = run_desc(desc, A, B, device, c_init=C0.copy(), c_dtype=torch.float32)
+    check(got, A, B, init=C0)
 
 
 RAGGED_SHAPES = [(1, 8, 8), (33, 24, 16), (97, 88, 40), (200, 136, 72),

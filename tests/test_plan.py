@@ -1,0 +1,216 @@
+"""Plan pipeline (tb-opt and tb_plan_from_mlir) on the CPU.
+
+Covers: the IR text as a lossless checkpoint (pass-by-pass runs through
+separate tb-opt processes equal one pipeline run; print/parse round trips),
+agreement of the contract lowering with the runtime's kernel binding and
+with the workloads' direct configurations, the diagnostics of every
+legality rule, and the contract verifier catching a tampered mainline.
+"""
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+import mini_triton_nvgpu_v1_amd as tb
+from mini_triton_nvgpu_v1_amd import configs
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+TB_OPT = ROOT / "mini_triton_nvgpu_v1_amd" / "bin" / "tb-opt"
+
+STAGE1_PASSES = [
+    "tb-verify-scope", "tb-attach-target-info{gpu-arch=gfx950}",
+    "tb-semanticize-matmul", "tb-build-program-mapping-plan",
+    "tb-build-layout-plan", "tb-build-transport-plan",
+    "tb-build-c-register-plan", "tb-rewrite-matmul-mainloop",
+    "tb-cleanup-layout-conversions", "tb-build-mainloop-graph",
+    "tb-regularize-k-loop", "tb-assign-latencies", "tb-schedule-loops",
+    "tb-derive-waits", "tb-expand-pipeline", "tb-cleanup-pipeline",
+    "tb-verify-pipeline-mainline-contract"]
+FULL = "builtin.module(tb-stage1-full-to-gfx950-pipeline{cubin-chip=gfx950})"
+MAINLINE = "builtin.module(" + ",".join(STAGE1_PASSES) + ")"
+
+
+def tb_opt(text, *args, check=True):
+    if not TB_OPT.exists():
+        pytest.fail("bin/tb-opt is not built (run __graft_entry__.build())")
+    p = subprocess.run([str(TB_OPT), "-", *args], input=text,
+                       capture_output=True, text=True, timeout=120)
+    if check and p.returncode != 0:
+        raise AssertionError(f"tb-opt {args} failed:\n{p.stderr}")
+    return p
+
+
+def matmul_module(M=64, N=64, K=32, bm=64, bn=64, bk=32, warps=4, stages=2,
+                  c="f16", exact=True, extra_module="", extra_op=""):
+    ex = "true" if exact else "false"
+    return (
+        f'module attributes {{"tb.num-warps" = {warps} : i64, '
+        f'"tb.requested-stages" = {stages} : i64{extra_module}}} {{\n'
+        f"  func.func @kernel(%A: memref<{M}x{K}xf16>, %B: memref<{K}x{N}xf16>,"
+        f" %C: memref<{M}x{N}x{c}>) {{\n"
+        f"    tb.matmul %A, %B, %C {{block_m = {bm} : i64, block_n = {bn} : i64,"
+        f" block_k = {bk} : i64, exact_tile = {ex}{extra_op}}}\n"
+        f"      : memref<{M}x{K}xf16>, memref<{K}x{N}xf16>, memref<{M}x{N}x{c}>\n"
+        f"    func.return\n  }}\n}}\n")
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_pass_by_pass_equals_pipeline(w):
+    """Every pass re-reads its inputs from the IR text: running the passes
+    one process at a time gives exactly the one-shot pipeline's output."""
+    text = w.mlir()
+    for p in STAGE1_PASSES:
+        text = tb_opt(text, f"--pass-pipeline=builtin.module({p})").stdout
+    one_shot = tb_opt(w.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+    assert text == one_shot
+    assert "tb.pipeline_mainline" in text and "tb.matmul " not in text
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_print_parse_roundtrip(w):
+    sealed = tb_opt(w.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+    assert tb_opt(sealed).stdout == sealed
+    lowered = tb_opt(w.mlir(), f"--pass-pipeline={FULL}").stdout
+    assert tb_opt(lowered).stdout == lowered
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_plan_config_matches_direct_config(w):
+    plan = tb.plan_from_mlir(w.mlir()).config
+    direct = w.direct_config()
+    for f, _ in type(plan)._fields_:
+        assert getattr(plan, f) == getattr(direct, f), f
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_lowering_names_the_bound_kernel(w, tmp_path):
+    lowered = tb_opt(w.mlir(), f"--pass-pipeline={FULL}").stdout
+    name = re.search(r'kernel = "([^"]+)"', lowered).group(1)
+    desc = tb.plan_from_mlir(w.mlir())
+    assert desc.kernel_name == name
+    lds = int(re.search(r"lds_bytes = (\d+)", lowered).group(1))
+    assert desc.lds_bytes == lds
+    ws = int(re.search(r"workspace_bytes = (\d+)", lowered).group(1))
+    assert desc.workspace_bytes == ws
+    # the lowered module and the sealed mainline both load as plan files
+    f = tmp_path / "lowered.mlir"
+    f.write_text(lowered)
+    assert tb.plan_from_file(str(f)).config == desc.config
+    g = tmp_path / "sealed.mlir"
+    g.write_text(tb_opt(w.mlir(), f"--pass-pipeline={MAINLINE}").stdout)
+    assert tb.plan_from_file(str(g)).config == desc.config
+
+
+def test_schedule_window_is_bounded():
+    """The buffer model covers min(k groups, stages + 1) groups, so the host
+    work does not grow with K (4096 and 8192 share the same plan size)."""
+    sizes = {}
+    for w in (configs.ROOFLINE, configs.PERSISTENT):
+        text = tb_opt(w.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+        window = min(-(-w.K // w.block[2]), w.stages + 1)
+        assert text.count("tb.async_issue_cluster") == window
+        assert text.count("tb.consumer_wait_cluster") == window
+        assert text.count("tb.mma_compute_cluster") == window
+        assert f"iteration_count = {-(-w.K // w.block[2])}" not in text  # loop plan dropped
+        sizes[w.name] = len(text)
+    assert abs(sizes["gemm_4096"] - sizes["persistent_8192"]) < 4096
+
+
+def test_cluster_order_refills_after_reads():
+    """Within a time slot the waits and MFMAs of the consumed group come
+    before the refill of its ring slot (clusters 0, 1, 2)."""
+    text = tb_opt(configs.ROOFLINE.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+    body = re.findall(r"tb\.(async_issue|consumer_wait|mma_compute)_cluster "
+                      r"\{cluster = (\d+) : i64, k_group = (\d+) : i64.*?"
+                      r"stage = (\d+) : i64", text)
+    S = configs.ROOFLINE.stages
+    seen = [(int(st), int(cl), k, int(g)) for k, cl, g, st in body]
+    assert seen == sorted(seen)
+    for st, cl, kind, g in seen:
+        if kind == "async_issue":
+            assert (st, cl) == (g, 2)
+        else:
+            assert st == g + S and cl == (0 if kind == "consumer_wait" else 1)
+
+
+ERRORS = [
+    ("sm86", matmul_module(), "--tb-attach-target-info=gpu-arch=sm_86",
+     "supports gpu-arch `gfx950`"),
+    ("no_arch", matmul_module(), "--tb-attach-target-info",
+     "requires explicit `gpu-arch`"),
+    ("block_m_48", matmul_module(M=96, bm=48, exact=False), FULL,
+     "block_m % 32 == 0"),
+    ("block_k_16", matmul_module(bk=16), FULL, "block_k in {32, 64}"),
+    ("inexact", matmul_module(M=96), FULL, "exact_tile=true requires"),
+    ("stages_5", matmul_module(stages=5), FULL, "num_stages in [2, 4]"),
+    ("lds_budget", matmul_module(M=256, N=256, K=64, bm=256, bn=256, bk=64,
+                                 stages=4), FULL, "exceed the target LDS budget"),
+    ("persistent_splitk", matmul_module(
+        K=64, extra_module=', "tb.persistent" = true, "tb.split-k" = 2 : i64'),
+     FULL, "persistent and split-k"),
+    ("bad_reduction", matmul_module(
+        K=64, extra_module=', "tb.split-k" = 2 : i64, "tb.reduction-mode" = "tree"'),
+     FULL, "must be `split_k_serial` or `split_k_parallel`"),
+    ("atomic_f16", matmul_module(
+        K=64, extra_module=', "tb.split-k" = 2 : i64, '
+        '"tb.reduction-mode" = "split_k_parallel"'),
+     FULL, "needs an f32 C"),
+    ("wave_grid", matmul_module(warps=3), FULL, "legal wave grid"),
+    ("f32_a", matmul_module().replace("memref<64x32xf16>", "memref<64x32xf32>"),
+     FULL, "fp16 x fp16"),
+    ("n_not_8", matmul_module(N=68, exact=False), FULL, "multiples of 8"),
+    ("out_of_order", matmul_module(), "--tb-build-layout-plan", "tb.target"),
+    ("unknown_pass", matmul_module(), "--tb-frobnicate", "unknown pass"),
+    ("bad_ir", "module {", FULL, "parse error"),
+]
+
+
+@pytest.mark.parametrize("name,text,arg,msg", ERRORS, ids=[e[0] for e in ERRORS])
+def test_diagnostics(name, text, arg, msg):
+    args = [f"--pass-pipeline={arg}"] if arg.startswith("builtin") else [arg]
+    p = tb_opt(text, *args, check=False)
+    assert p.returncode == 1, p.stdout[:500]
+    assert msg in p.stderr, p.stderr
+
+
+@pytest.mark.parametrize("name,text,arg,msg",
+                         [e for e in ERRORS if e[2] == FULL],
+                         ids=[e[0] for e in ERRORS if e[2] == FULL])
+def test_plan_from_mlir_diagnostics(name, text, arg, msg):
+    with pytest.raises(tb.TbError, match=re.escape(msg)):
+        tb.plan_from_mlir(text)
+
+
+def test_verifier_catches_tampering():
+    sealed = tb_opt(configs.ROOFLINE.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+    verify = "--tb-verify-pipeline-mainline-contract"
+    assert tb_opt(sealed, verify).returncode == 0
+    n = len(re.findall(r"tb\.async_issue_cluster", sealed))
+    bad = sealed.replace(f"async_groups = {n} : i64", f"async_groups = {n + 1} : i64")
+    p = tb_opt(bad, verify, check=False)
+    assert p.returncode == 1 and "async_groups" in p.stderr
+    # a refill scheduled before the last read of its slot
+    bad = re.sub(r"(tb\.async_issue_cluster \{cluster = )2", r"\g<1>0", sealed, count=4)
+    p = tb_opt(bad, verify, check=False)
+    assert p.returncode == 1 and "contract" in p.stderr
+    # the lowering refuses an LDS encoding the kernels do not implement
+    bad = sealed.replace("perPhase = 2, maxPhase = 8", "perPhase = 1, maxPhase = 8")
+    assert bad != sealed
+    p = tb_opt(bad, "--tb-lower-pipeline-to-gfx950", check=False)
+    assert p.returncode == 1 and "swizzle" in p.stderr
+
+
+def test_cleanup_layout_conversions():
+    text = (
+        'module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {\n'
+        "  func.func @kernel(%A: memref<64x32xf16>, %B: memref<32x64xf16>, %C: memref<64x64xf16>) {\n"
+        "    %0 = tb.convert_layout %A : (memref<64x32xf16>) -> memref<64x32xf16>\n"
+        "    %1 = tb.convert_layout %B : (memref<32x64xf16>) -> memref<32x64xf16, strided<[64, 1]>>\n"
+        "    %2 = tb.convert_layout %1 : (memref<32x64xf16, strided<[64, 1]>>) -> memref<32x64xf16>\n"
+        "    %3 = tb.convert_layout %C : (memref<64x64xf16>) -> memref<64x64xf16, strided<[64, 1]>>\n"
+        "    tb.matmul %0, %2, %C {block_m = 64 : i64, block_n = 64 : i64, block_k = 32 : i64, exact_tile = true} : memref<64x32xf16>, memref<32x64xf16>, memref<64x64xf16>\n"
+        "    return\n  }\n}\n")
+    out = tb_opt(text, "--tb-cleanup-layout-conversions").stdout
+    assert "tb.convert_layout" not in out
+    assert "tb.matmul %A, %B, %C" in out
