@@ -33,8 +33,10 @@ def log(msg: str) -> None:
 
 
 def time_workload(w, steps: int, warmup: int, device):
-    """Launch `w` steps times; wall clock over the timed region plus per-launch
-    HIP event durations recorded on the launch stream."""
+    """Launch `w` steps times back to back; wall clock over the timed region,
+    HIP events on the launch stream around the whole timed region (average
+    launch duration = elapsed / steps, the GPU never idles in between), and
+    per-launch events for the median of short kernels."""
     import torch
     import mini_triton_nvgpu_v1_amd as tb
 
@@ -50,20 +52,44 @@ def time_workload(w, steps: int, warmup: int, device):
     tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
     for _ in range(warmup):
         desc.launch(A, B, C, ws, stream=stream)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
+    region[0].record(stream)
     for i in range(steps):
+        desc.launch(A, B, C, ws, stream=stream)
+    region[1].record(stream)
+    torch.cuda.synchronize(device)
+    wall = time.perf_counter() - t0
+    avg_ms = region[0].elapsed_time(region[1]) / steps
+    # per-launch events (a separate pass, not part of the timed region)
+    n = min(steps, 50)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for i in range(n):
         starts[i].record(stream)
         desc.launch(A, B, C, ws, stream=stream)
         ends[i].record(stream)
     torch.cuda.synchronize(device)
-    wall = time.perf_counter() - t0
     durs_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     finite = bool(torch.isfinite(C).all().item())
-    return {"wall_s": wall, "kernel_ms": durs_ms, "kernel": desc.kernel_name,
-            "finite": finite}
+    return {"wall_s": wall, "avg_launch_ms": avg_ms, "kernel_ms": durs_ms,
+            "kernel": desc.kernel_name, "finite": finite}
+
+
+def plan_time_ms(w, reps: int = 20) -> float:
+    """Host time of the whole plan pipeline (parse, 17 passes, contract
+    lowering, kernel binding) for the workload's tb.matmul module: the
+    reference's CPU-side work on this path, single-threaded."""
+    import mini_triton_nvgpu_v1_amd as tb
+
+    text = w.mlir()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        tb.plan_from_mlir(text)
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e3
 
 
 def cpu_baseline(w, budget_s: float = 12.0):
@@ -123,8 +149,9 @@ def load_traffic(workload: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the timed region is ~40 ms; warm-up long enough for clocks to settle
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="gemm_4096")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -147,7 +174,7 @@ def main() -> int:
         return 1
     ms_per_step = r["wall_s"] * 1e3 / args.steps
     value = w.flop * args.steps / r["wall_s"] / 1e12
-    avg_kernel_ms = statistics.mean(r["kernel_ms"])
+    avg_kernel_ms = r["avg_launch_ms"]
     achieved = w.flop / (avg_kernel_ms * 1e-3) / 1e12
     log(f"bench: {r['kernel']} wall {ms_per_step * 1e3:.1f} us/step, "
         f"kernel avg {avg_kernel_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s")
@@ -166,6 +193,7 @@ def main() -> int:
                 "us_per_launch_kernel_median": round(kern_us, 2),
                 "tflops_kernel": round(other.flop / (kern_us * 1e-6) / 1e12, 2),
                 "frac_mfma_peak": round(other.flop / (kern_us * 1e-6) / 1e12 / PEAK_TFLOPS_F16, 4),
+                "plan_pipeline_ms": round(plan_time_ms(other), 3),
                 "kernel": o["kernel"], "finite": o["finite"]}
             log(f"bench: {other.name}: {extra[other.name]}")
 
@@ -192,7 +220,8 @@ def main() -> int:
                    "tile": list(w.block), "num_waves": w.num_waves,
                    "group_m": w.group_m, "split_k": w.split_k,
                    "persistent": w.persistent, "c_dtype": "f16",
-                   "accumulate": "f32", "kernel": r["kernel"]},
+                   "accumulate": "f32", "kernel": r["kernel"],
+                   "plan_pipeline_ms": round(plan_time_ms(w), 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_TFLOPS_F16, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS_F16, 4),

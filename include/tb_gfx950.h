@@ -93,17 +93,23 @@ const char *tb_last_error(void);
  * validation + gpu.func emission). */
 int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out);
 
-/* Run the unchanged tb plan pipeline (tb-verify-scope ... tb-cleanup-pipeline,
- * lib/Transforms/Stage1Pipelines.cpp:14-41) on a module holding one
- * tb.matmul, with tb-attach-target-info{gpu-arch=<gpu_arch>}, then flatten
- * the KernelContract (lib/Analysis/KernelContract.cpp:9-65) into a
- * descriptor. Leading dimensions default to the memref shapes. */
+/* Run the tb plan pipeline (tb-verify-scope ... tb-verify-pipeline-mainline-
+ * contract, the pass list of lib/Transforms/Stage1Pipelines.cpp:14-36) on a
+ * module holding one tb.matmul, with tb-attach-target-info{gpu-arch=
+ * <gpu_arch>} (NULL or "" = "gfx950"), then flatten the KernelContract
+ * (lib/Analysis/KernelContract.cpp:9-65) into a descriptor. A module that
+ * already holds a sealed tb.pipeline_mainline or a lowered tb.gfx950_launch
+ * is accepted as is. Operands are identity-layout memrefs, so the leading
+ * dimensions are the memref row lengths. Errors carry the pass name and the
+ * diagnostic (the reference's emitError text where the rule is shared). */
 int tb_plan_from_mlir(const char *mlir, size_t len, const char *gpu_arch,
                       tb_gemm_desc **out);
 
-/* Read the descriptor side-file that `tb-opt
- * --tb-lower-pipeline-to-gfx950=desc-file=<path>` writes (replaces the
- * extracted gpu.binary payload, tools/bench_stage1_fair.py:531-564). */
+/* Same, reading the module from a file: typically the output of
+ * `tb-opt --pass-pipeline='builtin.module(tb-stage1-full-to-gfx950-pipeline
+ * {cubin-chip=gfx950})'`, whose tb.gfx950_launch op replaces the gpu.binary
+ * payload the reference's harness extracts (tools/bench_stage1_fair.py:
+ * 531-564). */
 int tb_plan_from_file(const char *path, tb_gemm_desc **out);
 
 /* Copy the flattened config back out. */

@@ -72,34 +72,36 @@ def test_persistent_8192_parity_row_sample(device):
     check(got, A, B, rows=[(0, 40), (4080, 4128), (8150, 8192)])
 
 
-# Modules of the tb-opt contract tests with an f32 C, which the plan maps to
-# C += A B (the reference's tb.matmul semantics): C starts from a seeded
-# non-zero value and the oracle adds it.
+# The configurations of the reference's examples/*.mlir and contract tests
+# (f32 C, 1-4 warps), which the plan maps to C += A B, the reference's
+# tb.matmul semantics: C starts from a seeded non-zero value and the oracle
+# adds it. Plus a serial split-k with an uneven k-tile split.
 PLAN_MODULES = [
-    ("exact_f32_1wave", 64, 64, 32, 1, ""),
-    ("grouped_f32", 192, 128, 32, 4, ""),
-    ("ragged_f32_1wave", 96, 80, 32, 1, ""),
-    ("two_wave_f32", 64, 64, 32, 2, ""),
-    ("persistent_grouped_f32", 192, 128, 32, 4,
+    ("smoke_64x64x32_1wave", 64, 64, 32, 64, 1, ""),
+    ("smoke_128x128x32", 128, 128, 32, 128, 4, ""),
+    ("smoke_96x80x32_1wave", 96, 80, 32, 64, 1, ""),
+    ("grouped_192x128x32", 192, 128, 32, 64, 4, ""),
+    ("two_wave_64x64x32", 64, 64, 32, 64, 2, ""),
+    ("persistent_192x128x32", 192, 128, 32, 64, 4,
      ', "tb.persistent" = true, "tb.num-ctas" = 2 : i64'),
-    ("splitk_atomic_f32", 64, 64, 64, 1,
+    ("splitk_atomic_64x64x64", 64, 64, 64, 64, 1,
      ', "tb.split-k" = 2 : i64, "tb.reduction-mode" = "split_k_parallel"'),
-    ("splitk_serial_f32", 64, 64, 128, 1,
+    ("splitk_serial_64x64x128", 64, 64, 128, 64, 1,
      ', "tb.split-k" = 3 : i64, "tb.reduction-mode" = "split_k_serial"'),
 ]
 
 
-@pytest.mark.parametrize("name,M,N,K,warps,extra", PLAN_MODULES,
+@pytest.mark.parametrize("name,M,N,K,tile,warps,extra", PLAN_MODULES,
                          ids=[p[0] for p in PLAN_MODULES])
-def test_plan_module_f32_accumulate(name, M, N, K, warps, extra, device):
-    exact = "true" if M % 64 == 0 and N % 64 == 0 else "false"
-    gm = ", group_m = 2 : i64" if name == "grouped_f32" else ""
+def test_plan_module_f32_accumulate(name, M, N, K, tile, warps, extra, device):
+    exact = "true" if M % tile == 0 and N % tile == 0 else "false"
+    gm = ", group_m = 2 : i64" if name.startswith("grouped") else ""
     text = (
         f'module attributes {{"tb.num-warps" = {warps} : i64, '
         f'"tb.requested-stages" = 2 : i64{extra}}} {{\n'
         f"  func.func @kernel(%A: memref<{M}x{K}xf16>, %B: memref<{K}x{N}xf16>, "
         f"%C: memref<{M}x{N}xf32>) {{\n"
-        f"    tb.matmul %A, %B, %C {{block_m = 64 : i64, block_n = 64 : i64, "
+        f"    tb.matmul %A, %B, %C {{block_m = {tile} : i64, block_n = {tile} : i64, "
         f"block_k = 32 : i64, exact_tile = {exact}{gm}}} : memref<{M}x{K}xf16>, "
         f"memref<{K}x{N}xf16>, memref<{M}x{N}xf32>\n    return\n  }}\n}}\n")
     print(f"plan module {name}", flush=True)
