@@ -43,6 +43,11 @@ class Workload:
         return 2 * self.M * self.N * self.K
 
     @property
+    def algo_bytes(self) -> int:
+        """Algorithmic HBM bytes: A, B and the f16 C each moved once."""
+        return 2 * (self.M * self.K + self.K * self.N + self.M * self.N)
+
+    @property
     def scale(self) -> float:
         return 1.0 / math.sqrt(self.K) if self.dist == NORMAL else 1.0
 
