@@ -93,7 +93,7 @@ __device__ __forceinline__ void map_program(const GemmParams &p, int pid,
   part = 0;
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int STAGES>
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int SPREAD_REQ = -1>
 struct GemmTile {
   static constexpr int NW = WGM * WGN; // waves
   static constexpr int NT = NW * 64;
@@ -123,14 +123,45 @@ struct GemmTile {
   static constexpr int LA = A_STAGE / NT;
   static constexpr int LB = B_STAGE / NT;
   static constexpr int LPT = LA + LB;
-  // vmcnt allowed at the prologue wait / the per-tile barrier = loads issued
-  // after the tile being waited for (vmcnt retires in issue order): the
-  // prologue fills all STAGES stages; the loop waits for tile it+1 while
-  // tiles it+2 .. it+STAGES-1 may still be in flight.
-  static constexpr int VM_PROLOGUE = (STAGES - 1) * LPT;
-  static constexpr int VM_LOOP = (STAGES - 2) * LPT;
   static constexpr int A_ROWS_PER_LOAD = NT / KCH; // rows one load round covers
   static constexpr int B_ROWS_PER_LOAD = NT / BNC;
+
+  // ---- slot schedule (tiles with >= 4 MFMAs per k step) ------------------
+  // A k-tile is NSLOT MFMA slots (KSTEPS x NMFMA). The one barrier per
+  // k-tile sits before slot BQ, AFTER slots before the end. The refill of
+  // the LDS stage the barrier frees is spread over SPREAD slots from the
+  // barrier on: load l of that tile goes load_off(l) slots after the
+  // barrier, i.e. in the same k-tile while load_off(l) < AFTER, else in the
+  // next k-tile before its barrier. Spreading matters: the L2 -> CU path
+  // moves ~56 B/clk per CU and the kernel needs ~32 B/clk on average, so a
+  // burst of loads stalls the wave's issue (and its MFMAs) behind the queue.
+  static constexpr bool SLOTTED = NMFMA >= 4;
+  static constexpr int NSLOT = KSTEPS * NMFMA;
+  static constexpr int AFTER = NMFMA / 2;
+  static constexpr int BQ = NSLOT - AFTER;
+  // default spread: with 3+ stages the freed stage has a whole k-tile before
+  // its data is due; with 2 it is due at the next barrier, so the loads go
+  // out within one k step to leave the rest of the k-tile as latency slack
+  static constexpr int SPREAD =
+      SPREAD_REQ > 0 ? SPREAD_REQ : (STAGES >= 3 ? NSLOT : NMFMA);
+  static constexpr int load_off(int l) { return SPREAD * l / LPT; }
+  static constexpr int count_after() {
+    int n = 0;
+    for (int l = 0; l < LPT; ++l)
+      n += load_off(l) < AFTER ? 1 : 0;
+    return n;
+  }
+  // loads of a refill issued in the k-tile of its barrier
+  static constexpr int NA = SLOTTED ? count_after() : LPT;
+
+  // vmcnt allowed at the prologue wait / the per-tile barrier = loads issued
+  // after the tile being waited for (vmcnt retires in issue order). The loop
+  // waits for tile it+1 while tiles it+2 .. it+STAGES-1 may be in flight
+  // (the refill of tile it+STAGES-1 started after the previous barrier and
+  // finished before this one). The prologue issues tiles 0 .. STAGES-2 and
+  // the first NA loads of tile STAGES-1, then waits for tile 0.
+  static constexpr int VM_PROLOGUE = (STAGES - 2) * LPT + NA;
+  static constexpr int VM_LOOP = (STAGES - 2) * LPT;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
@@ -143,6 +174,8 @@ struct GemmTile {
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
   static_assert(VM_LOOP < 64 && VM_PROLOGUE < 64, "vmcnt range");
+  static_assert(!SLOTTED || (SPREAD >= 1 && SPREAD <= NSLOT),
+                "a refill must be issued before the next barrier");
 };
 
 template <int NMFMA, int NREAD, int NVMEM>
@@ -157,17 +190,19 @@ __device__ __forceinline__ void sched_step() {
   }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int STAGES>
+template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int STAGES,
+          int SPREAD_REQ = -1>
 __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
-  using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES>;
+  using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES, SPREAD_REQ>;
   constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
-                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LB = T::LB;
+                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LPT = T::LPT;
   __shared__ u32x4 lds[STAGES * T::STAGE];
   auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // wave index as a scalar: the LDS bases of the direct loads derive from it
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
   const u32x4 ra4 = rsrc_dwords(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
@@ -236,57 +271,76 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                                    (uint32_t)(n0 + b_lc * 8)) * 2u
                                 : kOob;
 
-    // Issue the direct loads of k-tile kt into LDS stage `stage`.
-    auto issue_tile = [&](int kt, int stage) {
+    // Direct load l (0 .. LPT-1) of k-tile kt into LDS stage `stage`:
+    // A load rounds first (l < LA), then B rounds.
+    auto issue_load = [&](int kt, int stage, int l) {
       const int k0 = kt * BK;
       const bool kt_ok = kt < kt_end;
       // LDS byte address of this wave's first 1 KiB block in the stage
       const uint32_t a_lds =
           (uint32_t)(uintptr_t)(TBK_LDS void *)stage_base(stage) + wave * 1024u;
-      const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
-#pragma unroll
-      for (int i = 0; i < LA; ++i) {
+      if (l < LA) {
+        const int i = l;
         const int lc = a_lchunk(i);
         const bool ok = kt_ok && (k0 + lc * 8) < p.K && i * T::A_ROWS_PER_LOAD < a_rows_left;
         load_lds16(ra4, a_lds + i * NW * 1024u, ok ? a_vrow + lc * 16u : kOob,
                    k0 * 2 + i * T::A_ROWS_PER_LOAD * p.lda * 2);
-      }
-#pragma unroll
-      for (int i = 0; i < LB; ++i) {
+      } else {
+        const int i = l - LA;
+        const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
         const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
         load_lds16(rb4, b_lds + i * NW * 1024u,
                    (kt_ok && krow < p.K) ? b_voff : kOob,
                    (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
       }
     };
+    auto issue_tile = [&](int kt, int stage) {
+#pragma unroll
+      for (int l = 0; l < LPT; ++l)
+        issue_load(kt, stage, l);
+    };
 
     half8 fa[2][TM], fb[2][TN];
-    auto read_frags = [&](int buf, int stage, int ks) {
+    // A fragment i of k step ks: one ds_read_b128
+    auto read_frag_a = [&](int buf, int stage, int ks, int i) {
       const TBK_LDS u32x4 *As = (const TBK_LDS u32x4 *)stage_base(stage);
-      const TBK_LDS char *Bs = (const TBK_LDS char *)(As + T::A_STAGE);
       const int c = ks * 2 + khalf;
+      const int row = fr_a + i * 32;
+      fa[buf][i] = __builtin_bit_cast(
+          half8, As[row * KCH + (c ^ ((row / T::A_PP) % KCH))]);
+    };
+    // B fragment j of k step ks: two ds_read_b64_tr_b16
+    auto read_frag_b = [&](int buf, int stage, int ks, int j) {
+      const TBK_LDS char *Bs =
+          (const TBK_LDS char *)((const TBK_LDS u32x4 *)stage_base(stage) + T::A_STAGE);
+      const int n = tr_n + j * 32;
+      half4 h[2];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = fr_a + i * 32;
-        fa[buf][i] = __builtin_bit_cast(
-            half8, As[row * KCH + (c ^ ((row / T::A_PP) % KCH))]);
+      for (int r = 0; r < 2; ++r) {
+        const int k = ks * 16 + tr_k + 4 * r;
+        const int pc = (n >> 3) ^ (4 * ((k / T::B_PP) % T::B_MAXPH));
+        const TBK_LDS short4 *src = (const TBK_LDS short4 *)(
+            Bs + k * (BN * 2) + pc * 16 + (n & 7) * 2);
+        h[r] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                             (TBK_LDS short4 *)src));
       }
+      fb[buf][j] = (half8){h[0][0], h[0][1], h[0][2], h[0][3],
+                           h[1][0], h[1][1], h[1][2], h[1][3]};
+    };
+    // fragment read r (0 .. TM+TN-1) in the order the MFMAs consume them:
+    // A0, B0 .. B(TN-1), A1 .. A(TM-1)
+    auto read_frag = [&](int buf, int stage, int ks, int r) {
+      if (r == 0)
+        read_frag_a(buf, stage, ks, 0);
+      else if (r <= TN)
+        read_frag_b(buf, stage, ks, r - 1);
+      else
+        read_frag_a(buf, stage, ks, r - TN);
+    };
+    auto read_frags = [&](int buf, int stage, int ks) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int n = tr_n + j * 32;
-        half4 h[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int k = ks * 16 + tr_k + 4 * r;
-          const int pc = (n >> 3) ^ (4 * ((k / T::B_PP) % T::B_MAXPH));
-          const TBK_LDS short4 *src = (const TBK_LDS short4 *)(
-              Bs + k * (BN * 2) + pc * 16 + (n & 7) * 2);
-          h[r] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                               (TBK_LDS short4 *)src));
-        }
-        fb[buf][j] = (half8){h[0][0], h[0][1], h[0][2], h[0][3],
-                             h[1][0], h[1][1], h[1][2], h[1][3]};
-      }
+      for (int r = 0; r < TM + TN; ++r)
+        read_frag(buf, stage, ks, r);
     };
     // C^T tile += B^T-fragment x A-fragment, i.e. C += A*B for this k step
     auto mfma_range = [&](int buf, int lo, int hi) {
@@ -300,12 +354,31 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       }
     };
 
-    // ---- prologue: tiles kt0 .. kt0+STAGES-1 in flight, one per stage ------
+    auto mfma_one = [&](int buf, int q) {
+      const int i = q / TN, j = q % TN;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i],
+                                                         acc[i][j], 0, 0, 0);
+    };
+
+    // ---- prologue ----------------------------------------------------------
+    // Slot schedule: tiles kt0 .. kt0+STAGES-2 whole plus the loads of tile
+    // kt0+STAGES-1 that its refill would issue after the barrier; burst
+    // schedule: tiles kt0 .. kt0+STAGES-1 whole. One stage per tile.
     if (persistent)
       __syncthreads(); // the previous tile's last fragment reads are done
+    if constexpr (T::SLOTTED) {
 #pragma unroll
-    for (int st = 0; st < STAGES; ++st)
-      issue_tile(kt0 + st, st);
+      for (int st = 0; st + 1 < STAGES; ++st)
+        issue_tile(kt0 + st, st);
+#pragma unroll
+      for (int l = 0; l < LPT; ++l)
+        if (T::load_off(l) < T::AFTER)
+          issue_load(kt0 + STAGES - 1, STAGES - 1, l);
+    } else {
+#pragma unroll
+      for (int st = 0; st < STAGES; ++st)
+        issue_tile(kt0 + st, st);
+    }
     wait_vmcnt<T::VM_PROLOGUE>();
     __syncthreads();
     read_frags(0, 0, 0);
@@ -315,11 +388,55 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // tiles stream into the other stages. Fragments are double-buffered
     // across the 16-deep k steps. The one barrier per k-tile sits in the
     // middle of the last k step: after it, tile it+1 (waited for with vmcnt
-    // before the barrier) is visible, and stage it % STAGES is free, so it is
-    // refilled with tile it+STAGES at once. All steps are unconditional
-    // (out-of-range tiles load zeros), so an iteration is one basic block
-    // the scheduler can interleave freely.
+    // before the barrier) is visible, and stage it % STAGES is free for tile
+    // it+STAGES. All steps are unconditional (out-of-range tiles load zeros).
     int s = 0;
+    if constexpr (T::SLOTTED) {
+      // Slot schedule: every MFMA slot is pinned in program order with the
+      // fragment reads and refill loads assigned to it (see GemmTile).
+      // Before the barrier, slot q also carries the loads of the refill that
+      // started after the previous barrier (tile it+STAGES-1, stage sp).
+      int sp = STAGES - 1;
+      for (int it = 0; it < nk; ++it) {
+        const int s_next = s + 1 == STAGES ? 0 : s + 1;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+          const int cur = ks & 1;
+#pragma unroll
+          for (int m = 0; m < NMFMA; ++m) {
+            const int q = ks * NMFMA + m;
+            if (q == T::BQ) {
+              wait_vmcnt<T::VM_LOOP>();
+              __syncthreads();
+            }
+            mfma_one(cur, m);
+            constexpr int R = TM + TN;
+            if (ks + 1 < KSTEPS) {
+#pragma unroll
+              for (int r = 0; r < R; ++r)
+                if (r * NMFMA / R == m)
+                  read_frag(cur ^ 1, s, ks + 1, r);
+            } else if (q >= T::BQ) {
+#pragma unroll
+              for (int r = 0; r < R; ++r)
+                if (T::BQ + r * T::AFTER / R == q)
+                  read_frag(cur ^ 1, s_next, 0, r);
+            }
+#pragma unroll
+            for (int l = 0; l < LPT; ++l) {
+              const int off = T::load_off(l);
+              if (off >= T::AFTER && off - T::AFTER == q)
+                issue_load(kt0 + it + STAGES - 1, sp, l);
+              if (off < T::AFTER && T::BQ + off == q)
+                issue_load(kt0 + it + STAGES, s, l);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        sp = s;
+        s = s_next;
+      }
+    } else
     for (int it = 0; it < nk; ++it) {
       const int s_next = s + 1 == STAGES ? 0 : s + 1;
 #pragma unroll
@@ -364,7 +481,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int i = 0; i < TM; ++i) {
         const int row = crow_base + i * 32;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int col = ccol_base + j * 32 + 8 * g;
@@ -382,6 +499,10 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                    ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
             __builtin_amdgcn_raw_buffer_store_b64(v, rc, off, 0, 0);
           }
+          // one 32x32 tile at a time: the conversions read the accumulators
+          // through VGPRs, and letting them run ahead needs a VGPR each
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {
       float *base = OUT == kOutF32Partial
@@ -394,7 +515,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int i = 0; i < TM; ++i) {
         const int row = crow_base + i * 32;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int col = ccol_base + j * 32 + 8 * g;
@@ -411,6 +532,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v),
                                                    rc, off, 0, 0);
           }
+          __builtin_amdgcn_sched_barrier(0); // one 32x32 tile at a time
+        }
       }
     } else { // kOutF32Atomic
       float *C = reinterpret_cast<float *>(p.C);

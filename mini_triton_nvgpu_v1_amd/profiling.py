@@ -22,6 +22,8 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--copy-reps", type=int, default=3)
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="also run torch.matmul on the same operands")
     args = ap.parse_args()
 
     import torch
@@ -52,6 +54,12 @@ def main() -> int:
         desc.launch(A, B, C, ws, stream=stream)
     torch.cuda.synchronize()
     print(f"profiling: {args.reps} launches of {desc.kernel_name} ({w.name})", flush=True)
+    if args.hipblaslt:
+        # the vendor library on the same operands, for side-by-side counters
+        for _ in range(args.reps):
+            torch.matmul(A, B, out=C)
+        torch.cuda.synchronize()
+        print(f"profiling: {args.reps} torch.matmul (hipBLASLt) launches", flush=True)
     return 0
 
 
