@@ -20,6 +20,30 @@ from . import (ACC_INIT_ZERO, DTYPE_F16, MAP_GROUPED_TILE,
 UNIFORM, NORMAL = 0, 1
 
 
+def wave_grid(block_m: int, block_n: int, num_waves: int, instr: int = 32):
+    """The plan's wave-grid choice: minimise |wave_tile_m - wave_tile_n| over
+    grids whose wave tiles are whole MFMA tiles, ties to more waves along the
+    longer block side (reference EncodingPlan.cpp:283-320)."""
+    best, best_score = None, None
+    for gm in range(1, num_waves + 1):
+        if num_waves % gm:
+            continue
+        gn = num_waves // gm
+        if block_m % gm or block_n % gn:
+            continue
+        tm, tn = block_m // gm, block_n // gn
+        if tm % instr or tn % instr:
+            continue
+        score = abs(tm - tn)
+        tie = best is not None and score == best_score and (
+            (block_m >= block_n and gm > best[0]) or (block_m < block_n and gn > best[1]))
+        if best is None or score < best_score or tie:
+            best, best_score = (gm, gn), score
+    if best is None:
+        raise ValueError("no legal wave grid")
+    return best
+
+
 @dataclass(frozen=True)
 class Workload:
     name: str
@@ -89,7 +113,7 @@ class Workload:
         (tb_plan_from_mlir on ``self.mlir()``); the tests check the two agree
         field by field."""
         bm, bn, bk = self.block
-        wg = {1: (1, 1), 2: (2, 1), 4: (2, 2), 8: (2, 4)}[self.num_waves]
+        wg = wave_grid(bm, bn, self.num_waves)
         tiles_m, tiles_n = -(-self.M // bm), -(-self.N // bn)
         if self.persistent:
             mapping = MAP_PERSISTENT_GROUPED
@@ -122,12 +146,16 @@ RAGGED = Workload("ragged_96x80x32", 96, 80, 32, 0x5EED0002, UNIFORM,
                   (64, 64, 32), num_waves=4, exact_tile=False)
 RAGGED_128 = Workload("tile_128x128x32", 128, 128, 32, 0x5EED0003, UNIFORM,
                       (128, 128, 32), num_waves=4)
+# 8 waves = 2 per SIMD on the 256x256 tile: one wave's MFMAs run while the
+# other waits on LDS reads or the barrier (~5% over 4 waves)
 ROOFLINE = Workload("gemm_4096", 4096, 4096, 4096, 0x5EED0004, NORMAL,
-                    (256, 256, 64), num_waves=4, stages=2, group_m=8)
+                    (256, 256, 64), num_waves=8, stages=2, group_m=8)
+# 128x64 tiles with 3 LDS stages: 32 tiles x 8 splits = 256 workgroups, one
+# per CU (128x128 tiles would leave half the CUs idle)
 SPLIT_K = Workload("splitk_512x512x16384", 512, 512, 16384, 0x5EED0005,
-                   UNIFORM, (128, 128, 64), num_waves=4, split_k=8)
+                   UNIFORM, (128, 64, 64), num_waves=4, stages=3, split_k=8)
 PERSISTENT = Workload("persistent_8192", 8192, 8192, 8192, 0x5EED0006, NORMAL,
-                      (256, 256, 64), num_waves=4, group_m=8, persistent=True,
+                      (256, 256, 64), num_waves=8, group_m=8, persistent=True,
                       num_ctas=256)
 
 ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]

@@ -3,6 +3,11 @@
 
 namespace tbk {
 static const KernelEntry kLarge[] = {
+    // 8 waves (2 per SIMD: one wave's MFMAs cover the other's waits), the
+    // grid the plan derives for 8 waves on a 256x256 tile
+    TBK_OUTS(256, 256, 64, 4, 2, 2),
+    TBK_OUTS(256, 256, 32, 4, 2, 3),
+    TBK_OUTS(256, 256, 32, 4, 2, 4),
     TBK_OUTS(256, 256, 64, 2, 2, 2),
     TBK_OUTS(256, 256, 32, 2, 2, 2),
     TBK_OUTS(256, 256, 32, 2, 2, 3),
