@@ -162,6 +162,11 @@ struct GemmTile {
   // the first NA loads of tile STAGES-1, then waits for tile 0.
   static constexpr int VM_PROLOGUE = (STAGES - 2) * LPT + NA;
   static constexpr int VM_LOOP = (STAGES - 2) * LPT;
+  // f16 C staged through LDS (256-byte wave-tile rows) when the ring holds
+  // every wave's tile; not for 128x128 wave tiles, whose 256 accumulator
+  // registers leave no room for the staging values
+  static constexpr bool STAGED_F16_EPILOGUE =
+      SLOTTED && WTN == 128 && WTM <= 64 && NW * WTM * 256 <= LDS_BYTES;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
@@ -474,7 +479,58 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // in acc[i][j][4g + r], h = lane / 32.
     const int crow_base = m0 + wm * T::WTM + (lane & 31);
     const int ccol_base = n0 + wn * T::WTN + 4 * khalf;
-    if constexpr (OUT == kOutF16) {
+    if constexpr (OUT == kOutF16 && T::STAGED_F16_EPILOGUE) {
+      // f16 C through LDS, so that every global store writes whole rows: a
+      // lane's 4 consecutive columns are only 8 bytes, and 8-byte pieces
+      // scattered over 32 rows write HBM lines partially. Each wave writes
+      // its WTM x 128 f16 tile into a private 256-byte-per-row LDS region
+      // (16-byte chunk c of row r at c ^ (r % 16), the two 8-byte halves of
+      // a chunk swapped when (r / 16) is odd: conflict-free for the 32-lane
+      // ds_write_b64 and the 16-lane ds_read_b128), then reads it back row
+      // by row, 16 lanes x 16 bytes per row, and stores 4 full rows per
+      // instruction.
+      __syncthreads(); // every wave drained its loads and finished its reads
+      TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * (T::WTM * 256);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const _Float16 h0 = (_Float16)acc[i][j][4 * g + 0];
+            const _Float16 h1 = (_Float16)acc[i][j][4 * g + 1];
+            const _Float16 h2 = (_Float16)acc[i][j][4 * g + 2];
+            const _Float16 h3 = (_Float16)acc[i][j][4 * g + 3];
+            u32x2 v;
+            v[0] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            v[1] = (uint32_t)__builtin_bit_cast(uint16_t, h2) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
+            const int chunk = (4 * j + g) ^ (r & 15);
+            const int half = khalf ^ ((r >> 4) & 1);
+            *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+          }
+          __builtin_amdgcn_sched_barrier(0); // one 32x32 tile at a time
+        }
+      }
+      const __amdgpu_buffer_rsrc_t rc =
+          make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
+      const int q = lane & 15;
+#pragma unroll
+      for (int it2 = 0; it2 < T::WTM / 4; ++it2) {
+        const int r = it2 * 4 + (lane >> 4);
+        u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
+        if ((r >> 4) & 1)
+          v = (u32x4){v[2], v[3], v[0], v[1]};
+        const int row = m0 + wm * T::WTM + r;
+        const int col = n0 + wn * T::WTN + 8 * q;
+        const uint32_t off = (row < p.M && col < p.N)
+                                 ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u
+                                 : kOob;
+        __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
+      }
+    } else if constexpr (OUT == kOutF16) {
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
 #pragma unroll
