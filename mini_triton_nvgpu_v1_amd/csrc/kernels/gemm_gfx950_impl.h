@@ -162,11 +162,16 @@ struct GemmTile {
   // the first NA loads of tile STAGES-1, then waits for tile 0.
   static constexpr int VM_PROLOGUE = (STAGES - 2) * LPT + NA;
   static constexpr int VM_LOOP = (STAGES - 2) * LPT;
-  // f16 C staged through LDS (256-byte wave-tile rows) when the ring holds
-  // every wave's tile; not for 128x128 wave tiles, whose 256 accumulator
-  // registers leave no room for the staging values
+  // f16 C staged through LDS (128- or 256-byte wave-tile rows) when the ring
+  // holds every wave's tile; not for 128x128 wave tiles, whose 256
+  // accumulator registers leave no room for the staging values
+  static constexpr int EPI_ROWB = WTN * 2;         // bytes per staged row
+  static constexpr int EPI_CPR = EPI_ROWB / 16;    // 16-byte chunks per row
+  static constexpr int EPI_RPP = 256 / EPI_ROWB;   // rows per 256-byte bank period
+  static constexpr int EPI_RPI = 64 / EPI_CPR;     // rows per 64-lane read
   static constexpr bool STAGED_F16_EPILOGUE =
-      SLOTTED && WTN == 128 && WTM <= 64 && NW * WTM * 256 <= LDS_BYTES;
+      SLOTTED && (WTN == 64 || WTN == 128) && WTM * WTN <= 8192 &&
+      NW * WTM * EPI_ROWB <= LDS_BYTES;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
@@ -483,14 +488,17 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       // f16 C through LDS, so that every global store writes whole rows: a
       // lane's 4 consecutive columns are only 8 bytes, and 8-byte pieces
       // scattered over 32 rows write HBM lines partially. Each wave writes
-      // its WTM x 128 f16 tile into a private 256-byte-per-row LDS region
-      // (16-byte chunk c of row r at c ^ (r % 16), the two 8-byte halves of
-      // a chunk swapped when (r / 16) is odd: conflict-free for the 32-lane
-      // ds_write_b64 and the 16-lane ds_read_b128), then reads it back row
-      // by row, 16 lanes x 16 bytes per row, and stores 4 full rows per
+      // its WTM x WTN f16 tile into a private LDS region of EPI_ROWB bytes
+      // per row. Row r's 16-byte chunk c sits at c ^ ((r / EPI_RPP) %
+      // EPI_CPR), and the two 8-byte halves of a chunk are swapped when
+      // (r / 16) is odd. The 32 lanes of a ds_write_b64 half (rows r..r+31,
+      // one chunk) then cover all 64 banks once, and so do the 16 lanes of a
+      // ds_read_b128 quarter (whole rows). The tile is read back row by row,
+      // EPI_CPR lanes x 16 bytes per row, and stored EPI_RPI full rows per
       // instruction.
       __syncthreads(); // every wave drained its loads and finished its reads
-      TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * (T::WTM * 256);
+      TBK_LDS char *wl =
+          (TBK_LDS char *)(TBK_LDS void *)lds + wave * (T::WTM * T::EPI_ROWB);
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = i * 32 + (lane & 31);
@@ -507,20 +515,21 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                    ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
             v[1] = (uint32_t)__builtin_bit_cast(uint16_t, h2) |
                    ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
-            const int chunk = (4 * j + g) ^ (r & 15);
+            const int chunk = (4 * j + g) ^ ((r / T::EPI_RPP) & (T::EPI_CPR - 1));
             const int half = khalf ^ ((r >> 4) & 1);
-            *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+            *(TBK_LDS u32x2 *)(wl + r * T::EPI_ROWB + chunk * 16 + half * 8) = v;
           }
           __builtin_amdgcn_sched_barrier(0); // one 32x32 tile at a time
         }
       }
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
-      const int q = lane & 15;
+      const int q = lane % T::EPI_CPR;
 #pragma unroll
-      for (int it2 = 0; it2 < T::WTM / 4; ++it2) {
-        const int r = it2 * 4 + (lane >> 4);
-        u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
+      for (int it2 = 0; it2 < T::WTM / T::EPI_RPI; ++it2) {
+        const int r = it2 * T::EPI_RPI + lane / T::EPI_CPR;
+        const int chunk = q ^ ((r / T::EPI_RPP) & (T::EPI_CPR - 1));
+        u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * T::EPI_ROWB + chunk * 16);
         if ((r >> 4) & 1)
           v = (u32x4){v[2], v[3], v[0], v[1]};
         const int row = m0 + wm * T::WTM + r;
