@@ -49,16 +49,22 @@ def time_workload(w, steps: int, warmup: int, device):
     ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=device)
           if desc.workspace_bytes else None)
     stream = torch.cuda.current_stream(device)
+    bias = None
+    if w.bias:  # fused bias step: N seeded values
+        bias = torch.empty((1, w.N), dtype=torch.float16, device=device)
+        tb.fill_seeded_f16(bias, 1, w.N, w.seed ^ 0xB1A5, 0, 1.0, stream=stream)
+        if w.bias == "f32":
+            bias = bias.float()
     tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
     tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
     for _ in range(warmup):
-        desc.launch(A, B, C, ws, stream=stream)
+        desc.launch(A, B, C, ws, stream=stream, bias=bias)
     region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
     region[0].record(stream)
     for i in range(steps):
-        desc.launch(A, B, C, ws, stream=stream)
+        desc.launch(A, B, C, ws, stream=stream, bias=bias)
     region[1].record(stream)
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
@@ -172,7 +178,7 @@ def main() -> int:
 
     extra = {}
     if not args.no_extra:
-        for other in configs.ALL:
+        for other in configs.ALL + configs.FUSED:
             if other.name == w.name:
                 continue
             steps = 200 if other.flop < 1e9 else (50 if other.flop < 2e11 else 10)

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TB_GFX950_ABI_VERSION 1
+#define TB_GFX950_ABI_VERSION 2
 
 /* element types (reference ScalarKind, include/tb/Analysis/KernelConfig.h:13-16) */
 #define TB_DTYPE_F16 0
@@ -63,6 +63,22 @@ extern "C" {
 #define TB_RED_WORKSPACE 1
 #define TB_RED_ATOMIC 2
 
+/* fused epilogue steps (reference EpilogueExprKind LoadBias + Add,
+ * Activation, Clamp; include/tb/Analysis/EpiloguePlan.h:61-75). They apply
+ * to the f32 result in the order bias, activation, clamp, before C is
+ * written (after C's prior value is added when acc_init is LOAD_C). The
+ * reference declares these exprs but derives none; here tb.matmul's
+ * `epilogue_*` attrs request them. */
+#define TB_EPI_BIAS_NONE 0
+#define TB_EPI_BIAS_F16 1 /* bias: N f16 values, C[r][c] += bias[c] */
+#define TB_EPI_BIAS_F32 2 /* bias: N f32 values */
+#define TB_ACT_NONE 0
+#define TB_ACT_RELU 1      /* max(x, 0) */
+#define TB_ACT_GELU_TANH 2 /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) */
+#define TB_ACT_SILU 3      /* x / (1 + exp(-x)) */
+#define TB_CLAMP_MIN 1     /* epi_clamp bits: x = max(x, clamp_min) */
+#define TB_CLAMP_MAX 2     /*                 x = min(x, clamp_max) */
+
 /* Flattened KernelContract: everything the gfx950 kernels consume. Mirrors
  * the fields the reference's lowering reads out of the plans
  * (LoweringContract, lib/Transforms/LowerPipelineToNVGPU.cpp:45-113). */
@@ -81,6 +97,10 @@ typedef struct tb_gemm_config {
   int32_t reduction;     /* TB_RED_* */
   int64_t num_programs;  /* workgroups launched (persistent: resident) */
   int32_t xcd_remap;     /* >1: remap program ids so neighbours share an XCD */
+  int32_t epi_bias;      /* TB_EPI_BIAS_* */
+  int32_t epi_activation; /* TB_ACT_* */
+  int32_t epi_clamp;     /* TB_CLAMP_* bits */
+  float clamp_min, clamp_max; /* finite, clamp_min <= clamp_max when both */
 } tb_gemm_config;
 
 typedef struct tb_gemm_desc tb_gemm_desc;
@@ -124,9 +144,20 @@ int64_t tb_desc_lds_bytes(const tb_gemm_desc *desc);
  * ReductionPlan scratchBytes (lib/Analysis/ReductionPlan.cpp:158-177). */
 size_t tb_workspace_bytes(const tb_gemm_desc *desc);
 
-/* Enqueue C = A*B (or C += A*B for TB_ACC_INIT_LOAD_C) on `stream`. */
+/* Enqueue C = A*B (or C += A*B for TB_ACC_INIT_LOAD_C) on `stream`, then
+ * the fused epilogue steps of the config. Fails for a config with a bias
+ * (use tb_gemm_launch_ex). Reference: the launcher of the lowered kernel,
+ * tools/bench_stage1_fair.py:665-699 (A, B, C device pointers). */
 int tb_gemm_launch(const tb_gemm_desc *desc, const void *a, const void *b,
                    void *c, void *workspace, void *stream);
+
+/* tb_gemm_launch plus the bias vector the epilogue reads (N elements of the
+ * config's bias type; NULL when the config has no bias). No reference
+ * counterpart: the reference's EpilogueExprKind::LoadBias
+ * (include/tb/Analysis/EpiloguePlan.h:61-67) names a bias operand that its
+ * tb.matmul never takes. */
+int tb_gemm_launch_ex(const tb_gemm_desc *desc, const void *a, const void *b,
+                      void *c, const void *bias, void *workspace, void *stream);
 
 void tb_desc_free(tb_gemm_desc *desc);
 

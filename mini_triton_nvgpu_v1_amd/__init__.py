@@ -22,6 +22,8 @@ __all__ = [
     "DTYPE_F16", "DTYPE_F32", "ACC_INIT_ZERO", "ACC_INIT_LOAD_C", "MAP_TILE",
     "MAP_GROUPED_TILE", "MAP_SPLIT_K", "MAP_PERSISTENT_TILE",
     "MAP_PERSISTENT_GROUPED", "RED_NONE", "RED_WORKSPACE", "RED_ATOMIC",
+    "EPI_BIAS_NONE", "EPI_BIAS_F16", "EPI_BIAS_F32", "ACT_NONE", "ACT_RELU",
+    "ACT_GELU_TANH", "ACT_SILU", "CLAMP_MIN", "CLAMP_MAX",
 ]
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -33,6 +35,10 @@ ACC_INIT_ZERO, ACC_INIT_LOAD_C = 0, 1
 (MAP_TILE, MAP_GROUPED_TILE, MAP_SPLIT_K, MAP_PERSISTENT_TILE,
  MAP_PERSISTENT_GROUPED) = range(5)
 RED_NONE, RED_WORKSPACE, RED_ATOMIC = 0, 1, 2
+# fused epilogue steps (bias, activation, clamp), applied in that order
+EPI_BIAS_NONE, EPI_BIAS_F16, EPI_BIAS_F32 = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
+CLAMP_MIN, CLAMP_MAX = 1, 2
 
 
 class TbError(RuntimeError):
@@ -52,6 +58,9 @@ class GemmConfig(ctypes.Structure):
         ("group_m", ctypes.c_int64), ("split_k", ctypes.c_int64),
         ("reduction", ctypes.c_int32), ("num_programs", ctypes.c_int64),
         ("xcd_remap", ctypes.c_int32),
+        ("epi_bias", ctypes.c_int32), ("epi_activation", ctypes.c_int32),
+        ("epi_clamp", ctypes.c_int32), ("clamp_min", ctypes.c_float),
+        ("clamp_max", ctypes.c_float),
     ]
 
     def as_dict(self) -> dict:
@@ -105,6 +114,8 @@ def lib() -> ctypes.CDLL:
     L.tb_workspace_bytes.restype = ctypes.c_size_t
     L.tb_gemm_launch.argtypes = [vp, vp, vp, vp, vp, vp]
     L.tb_gemm_launch.restype = ctypes.c_int
+    L.tb_gemm_launch_ex.argtypes = [vp, vp, vp, vp, vp, vp, vp]
+    L.tb_gemm_launch_ex.restype = ctypes.c_int
     L.tb_desc_free.argtypes = [vp]
     L.tb_desc_free.restype = None
     L.tb_fill_seeded_f16.argtypes = [vp, i64, i64, i64, ctypes.c_uint64, i32,
@@ -175,10 +186,17 @@ class GemmDesc:
     def workspace_bytes(self) -> int:
         return lib().tb_workspace_bytes(self._h)
 
-    def launch(self, a, b, c, workspace=None, stream=None) -> None:
-        """Enqueue C = A*B (or C += A*B) for device tensors/addresses."""
-        _check(lib().tb_gemm_launch(self._h, _ptr(a), _ptr(b), _ptr(c),
-                                    _ptr(workspace), _stream_handle(stream)))
+    def launch(self, a, b, c, workspace=None, stream=None, bias=None) -> None:
+        """Enqueue C = A*B (or C += A*B), then the config's fused epilogue
+        steps, for device tensors/addresses. ``bias`` (N values) is required
+        exactly when the config adds one."""
+        if bias is None:
+            _check(lib().tb_gemm_launch(self._h, _ptr(a), _ptr(b), _ptr(c),
+                                        _ptr(workspace), _stream_handle(stream)))
+        else:
+            _check(lib().tb_gemm_launch_ex(self._h, _ptr(a), _ptr(b), _ptr(c),
+                                           _ptr(bias), _ptr(workspace),
+                                           _stream_handle(stream)))
 
     def close(self) -> None:
         if self._h and self._h.value:

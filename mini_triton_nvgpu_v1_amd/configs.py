@@ -10,12 +10,18 @@ Each workload is a ``tb.matmul`` module (the reference's own input format,
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass, field
 
-from . import (ACC_INIT_ZERO, DTYPE_F16, MAP_GROUPED_TILE,
-               MAP_PERSISTENT_GROUPED, MAP_SPLIT_K, MAP_TILE, RED_NONE,
-               RED_WORKSPACE, GemmConfig)
+from . import (ACC_INIT_ZERO, ACT_GELU_TANH, ACT_NONE, ACT_RELU, ACT_SILU,
+               CLAMP_MAX, CLAMP_MIN, DTYPE_F16, EPI_BIAS_F16, EPI_BIAS_F32,
+               EPI_BIAS_NONE, MAP_GROUPED_TILE, MAP_PERSISTENT_GROUPED,
+               MAP_SPLIT_K, MAP_TILE, RED_NONE, RED_WORKSPACE, GemmConfig)
+
+ACTIVATIONS = {"": ACT_NONE, "relu": ACT_RELU, "gelu_tanh": ACT_GELU_TANH,
+               "silu": ACT_SILU}
+BIAS_KINDS = {"": EPI_BIAS_NONE, "f16": EPI_BIAS_F16, "f32": EPI_BIAS_F32}
 
 UNIFORM, NORMAL = 0, 1
 
@@ -61,6 +67,11 @@ class Workload:
     persistent: bool = False
     num_ctas: int = 1
     module_attrs: dict = field(default_factory=dict)
+    # fused epilogue steps (tb.matmul `epilogue_*` attrs)
+    bias: str = ""          # "", "f16" or "f32"
+    activation: str = ""    # "", "relu", "gelu_tanh" or "silu"
+    clamp_min: float | None = None
+    clamp_max: float | None = None
 
     @property
     def flop(self) -> int:
@@ -96,6 +107,14 @@ class Workload:
         a, b, c = (f"memref<{M}x{K}xf16>", f"memref<{K}x{N}xf16>",
                    f"memref<{M}x{N}x{c_type}>")
         gm = f",\n                          group_m = {self.group_m} : i64"
+        if self.bias:
+            gm += f',\n                          epilogue_bias = "{self.bias}"'
+        if self.activation:
+            gm += f',\n                          epilogue_activation = "{self.activation}"'
+        if self.clamp_min is not None:
+            gm += f",\n                          epilogue_clamp_min = {float(self.clamp_min)!r} : f32"
+        if self.clamp_max is not None:
+            gm += f",\n                          epilogue_clamp_max = {float(self.clamp_max)!r} : f32"
         return (
             f"module attributes {{{mattr}}} {{\n"
             f"  func.func @kernel(%A: {a}, %B: {b},\n"
@@ -137,7 +156,12 @@ class Workload:
             reduction=RED_WORKSPACE if self.split_k > 1 else RED_NONE,
             num_programs=programs,
             # XCD-aware program order once the tiles outnumber the 256 CUs
-            xcd_remap=8 if tiles_m * tiles_n > 256 else 0)
+            xcd_remap=8 if tiles_m * tiles_n > 256 else 0,
+            epi_bias=BIAS_KINDS[self.bias],
+            epi_activation=ACTIVATIONS[self.activation],
+            epi_clamp=(CLAMP_MIN if self.clamp_min is not None else 0)
+            | (CLAMP_MAX if self.clamp_max is not None else 0),
+            clamp_min=self.clamp_min or 0.0, clamp_max=self.clamp_max or 0.0)
 
 
 SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,
@@ -159,4 +183,8 @@ PERSISTENT = Workload("persistent_8192", 8192, 8192, 8192, 0x5EED0006, NORMAL,
                       num_ctas=256)
 
 ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]
-BY_NAME = {w.name: w for w in ALL}
+# The roofline GEMM with fused epilogue steps (a bias row and the tanh GELU
+# on the f32 result before the f16 store): what the fusion costs.
+FUSED = [dataclasses.replace(ROOFLINE, name="gemm_4096_bias_gelu", bias="f16",
+                             activation="gelu_tanh")]
+BY_NAME = {w.name: w for w in ALL + FUSED}

@@ -3,6 +3,8 @@
 #include "attr.h"
 
 #include <cctype>
+#include <cstdio>
+#include <cstdlib>
 #include <sstream>
 
 namespace tb {
@@ -22,6 +24,12 @@ AttrP IntU(int64_t v) {
   auto a = make(AttrKind::Int);
   a->i = v;
   a->itype = "";
+  return a;
+}
+AttrP F32(double v) {
+  auto a = make(AttrKind::Float);
+  a->f = (double)(float)v;
+  a->itype = "f32";
   return a;
 }
 AttrP Bool(bool v) {
@@ -97,6 +105,19 @@ std::string printKey(const std::string &k) { return bareKey(k) ? k : quote(k); }
 
 static void printTo(std::ostringstream &os, const AttrP &a);
 
+// MLIR's float attribute text: scientific notation with six fraction digits
+// when that reads back to the same value of the attribute's type, else as
+// many digits as the type needs to round-trip.
+static std::string printFloat(double v, const std::string &type) {
+  char buf[64];
+  snprintf(buf, sizeof buf, "%.6e", v);
+  const double back = strtod(buf, nullptr);
+  const bool same = type == "f32" ? (float)back == (float)v : back == v;
+  if (!same)
+    snprintf(buf, sizeof buf, type == "f32" ? "%.8e" : "%.16e", v);
+  return buf;
+}
+
 static void printParams(std::ostringstream &os, const Fields &params) {
   os << "<";
   bool first = true;
@@ -116,6 +137,9 @@ static void printTo(std::ostringstream &os, const AttrP &a) {
     os << a->i;
     if (!a->itype.empty())
       os << " : " << a->itype;
+    return;
+  case AttrKind::Float:
+    os << printFloat(a->f, a->itype) << " : " << a->itype;
     return;
   case AttrKind::Bool:
     os << (a->b ? "true" : "false");
@@ -393,6 +417,33 @@ AttrP parseAttr(ParseCursor &c) {
   if (ch == '!')
     return parseType(c);
   if (ch == '-' || std::isdigit((unsigned char)ch)) {
+    // a float literal has a fraction or an exponent: `-1.5`, `6.000000e+00`
+    size_t q = c.pos + (ch == '-' ? 1 : 0);
+    while (q < c.src.size() && std::isdigit((unsigned char)c.src[q]))
+      ++q;
+    if (q < c.src.size() && (c.src[q] == '.' || c.src[q] == 'e' || c.src[q] == 'E')) {
+      const char *begin = c.src.c_str() + c.pos;
+      char *end = nullptr;
+      const double v = strtod(begin, &end);
+      if (end == begin)
+        c.fail("expected a float literal");
+      c.pos += (size_t)(end - begin);
+      auto a = std::make_shared<Attr>();
+      a->kind = AttrKind::Float;
+      a->itype = "f64";
+      size_t save = c.pos;
+      if (c.consume(":")) {
+        c.skipWs();
+        if (c.consume("f32"))
+          a->itype = "f32";
+        else if (c.consume("f64"))
+          a->itype = "f64";
+        else
+          c.pos = save;
+      }
+      a->f = a->itype == "f32" ? (double)(float)v : v;
+      return a;
+    }
     int64_t v = c.integer();
     size_t save = c.pos;
     if (c.consume(":")) {
@@ -461,6 +512,14 @@ bool getBool(const Attr &dict, const std::string &name) {
   if (a.kind != AttrKind::Bool)
     throw Error("missing bool field `" + name + "`");
   return a.b;
+}
+double getF64(const Attr &dict, const std::string &name) {
+  const Attr &a = field(dict, name);
+  if (a.kind == AttrKind::Float)
+    return a.f;
+  if (a.kind == AttrKind::Int)
+    return (double)a.i;
+  throw Error("missing float field `" + name + "`");
 }
 std::string getStr(const Attr &dict, const std::string &name) {
   const Attr &a = field(dict, name);

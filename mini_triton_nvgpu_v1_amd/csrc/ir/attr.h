@@ -6,6 +6,7 @@
 // so this is a small self-contained value model that prints the same syntax
 // MLIR prints for the attribute kinds the plans use:
 //   integer      `5 : i64`      (untyped inside #tb.* parameter lists: `5`)
+//   float        `6.000000e+00 : f32`
 //   bool         `true`
 //   string       `"x"`
 //   dense i64    `array<i64: 1, 2>`
@@ -34,12 +35,14 @@ struct Attr;
 using AttrP = std::shared_ptr<const Attr>;
 using Fields = std::vector<std::pair<std::string, AttrP>>;
 
-enum class AttrKind { Int, Bool, String, DenseI64, Array, Dict, Dialect, Type, Unit };
+enum class AttrKind { Int, Float, Bool, String, DenseI64, Array, Dict, Dialect, Type, Unit };
 
 struct Attr {
   AttrKind kind = AttrKind::Unit;
   int64_t i = 0;
-  std::string itype = "i64"; // Int: "i64", "i32", "index" or "" (untyped)
+  std::string itype = "i64"; // Int: "i64", "i32", "index" or "" (untyped);
+                             // Float: "f32" or "f64"
+  double f = 0.0;
   bool b = false;
   std::string s; // String value, Type text, Dialect mnemonic ("shared")
   std::vector<int64_t> ints;   // DenseI64
@@ -52,6 +55,7 @@ struct Attr {
 // ---- constructors --------------------------------------------------------
 AttrP I64(int64_t v);
 AttrP IntU(int64_t v); // untyped integer (dialect parameter / array element)
+AttrP F32(double v); // float attribute of type f32 (value rounded to f32)
 AttrP Bool(bool v);
 AttrP Str(const std::string &v);
 AttrP Dense(const std::vector<int64_t> &v);
@@ -95,6 +99,7 @@ const Attr &field(const Attr &dict, const std::string &name);
 bool has(const Attr &dict, const std::string &name);
 int64_t getI64(const Attr &dict, const std::string &name);
 bool getBool(const Attr &dict, const std::string &name);
+double getF64(const Attr &dict, const std::string &name); // float or integer
 std::string getStr(const Attr &dict, const std::string &name);
 std::vector<int64_t> getDense(const Attr &dict, const std::string &name);
 const std::vector<AttrP> &getArr(const Attr &dict, const std::string &name);

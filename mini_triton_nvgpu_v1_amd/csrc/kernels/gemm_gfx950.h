@@ -59,10 +59,65 @@ struct GemmParams {
   int total_work; // programs (non-persistent) or work items (persistent)
   int xcds;       // > 1: remap program ids so neighbours share an XCD
   int ws_ld;      // leading dimension of the f32 partial output (elements)
+  // fused epilogue: bias (0 none, 1 f16, 2 f32; N values), activation
+  // (0 none, 1 relu, 2 gelu_tanh, 3 silu), clamp bits (1 min, 2 max)
+  const void *bias;
+  int epi_bias, epi_act, epi_clamp;
+  float clamp_lo, clamp_hi;
 };
+
+// The fused epilogue steps on 4 consecutive columns (col .. col+3) of one
+// row, in order bias, activation, clamp. Callers only reach this when at
+// least one step is set; every branch is on kernel arguments (wave-uniform).
+struct EpiArgs {
+  const void *bias;
+  int bias_kind, act, clamp;
+  float lo, hi;
+};
+
+__device__ __forceinline__ float epi_activation(float x, int act) {
+  if (act == 1)
+    return x > 0.f ? x : 0.f;
+  if (act == 2) { // tanh form of GELU (Hendrycks & Gimpel, 2016)
+    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.f + tanhf(u));
+  }
+  if (act == 3)
+    return x / (1.f + expf(-x));
+  return x;
+}
+
+typedef float epi_f32x4 __attribute__((ext_vector_type(4)));
+
+// Bias values of columns col .. col+3 (zero past N: those columns are never
+// stored). N % 4 == 0, so a group is wholly inside or outside.
+__device__ __forceinline__ epi_f32x4 epi_load_bias(const EpiArgs &e, int col, int N) {
+  epi_f32x4 b = {0.f, 0.f, 0.f, 0.f};
+  if (e.bias_kind == 0 || col >= N)
+    return b;
+  if (e.bias_kind == 1) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = *reinterpret_cast<const h4 *>(static_cast<const _Float16 *>(e.bias) + col);
+    b = (epi_f32x4){(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+  } else {
+    b = *reinterpret_cast<const epi_f32x4 *>(static_cast<const float *>(e.bias) + col);
+  }
+  return b;
+}
+
+__device__ __forceinline__ float epi_apply1(float x, float bias, const EpiArgs &e) {
+  x += bias;
+  x = epi_activation(x, e.act);
+  if (e.clamp & 1)
+    x = x < e.lo ? e.lo : x;
+  if (e.clamp & 2)
+    x = x > e.hi ? e.hi : x;
+  return x;
+}
 
 struct KernelKey {
   int bm, bn, bk, wgm, wgn, out, stages;
+  int epi; // 1: the fused epilogue steps are compiled in
 };
 
 struct KernelEntry {
@@ -76,9 +131,10 @@ const KernelEntry *find_kernel(const KernelKey &k);
 int kernel_count();
 const KernelEntry *kernel_at(int i);
 
-// C = [C +] sum_{p < split_k} ws[p] in fixed p order, cast to C's type.
+// C = epilogue([C +] sum_{p < split_k} ws[p]) in fixed p order, cast to C's type.
 hipError_t launch_reduce_ex(const float *ws, void *C, int M, int N, int ldc,
-                            int split_k, int c_f16, int load_c, hipStream_t s);
+                            int split_k, int c_f16, int load_c, const EpiArgs &epi,
+                            hipStream_t s);
 hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
                        uint64_t seed, int dist, double scale, hipStream_t s);
 

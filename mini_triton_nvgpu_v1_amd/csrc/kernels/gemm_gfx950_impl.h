@@ -200,8 +200,11 @@ __device__ __forceinline__ void sched_step() {
   }
 }
 
+// EPI: the fused epilogue steps (bias, activation, clamp) are compiled in.
+// Plain instances carry none of that code, so their register allocation is
+// the main loop's alone.
 template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int STAGES,
-          int SPREAD_REQ = -1>
+          int SPREAD_REQ = -1, bool EPI = false>
 __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES, SPREAD_REQ>;
   constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
@@ -484,6 +487,32 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // in acc[i][j][4g + r], h = lane / 32.
     const int crow_base = m0 + wm * T::WTM + (lane & 31);
     const int ccol_base = n0 + wn * T::WTN + 4 * khalf;
+
+    // Fused epilogue steps (bias, activation, clamp) on the whole f32 result,
+    // in place on the accumulators, one 32-column tile j at a time so a lane
+    // holds only that tile's 16 bias values. C += A*B applies them in its
+    // store loop, after the prior C is added. EPI instances are never
+    // launched for split-K partials (the reduction applies the steps there)
+    // nor with atomic output.
+    const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
+    if constexpr (EPI && (OUT == kOutF16 || OUT == kOutF32Partial)) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        epi_f32x4 bv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          bv[g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[i][j][4 * g + r] = epi_apply1(acc[i][j][4 * g + r], bv[g][r], ea);
+        __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
+      }
+    }
+
     if constexpr (OUT == kOutF16 && T::STAGED_F16_EPILOGUE) {
       // f16 C through LDS, so that every global store writes whole rows: a
       // lane's 4 consecutive columns are only 8 bytes, and 8-byte pieces
@@ -593,6 +622,12 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
               const f32x4 old = __builtin_bit_cast(
                   f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
               v += old;
+              if constexpr (EPI) {
+                const epi_f32x4 b = epi_load_bias(ea, col, p.N);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  v[r] = epi_apply1(v[r], b[r], ea);
+              }
             }
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v),
                                                    rc, off, 0, 0);
@@ -628,7 +663,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 
 // One registry entry per instance.
 #define TBK_ENTRY(BM, BN, BK, WGM, WGN, OUT, ST)                                 \
-  {{BM, BN, BK, WGM, WGN, OUT, ST},                                              \
+  {{BM, BN, BK, WGM, WGN, OUT, ST, 0},                                           \
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST>),                        \
    "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT}
@@ -637,3 +672,17 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   TBK_ENTRY(BM, BN, BK, WGM, WGN, 0, ST), TBK_ENTRY(BM, BN, BK, WGM, WGN, 1, ST), \
       TBK_ENTRY(BM, BN, BK, WGM, WGN, 2, ST),                                   \
       TBK_ENTRY(BM, BN, BK, WGM, WGN, 3, ST)
+
+// Fused-epilogue instances: f16 C, plain f32 C, and f32 C += A*B (atomic
+// split-K cannot carry the steps; split-K partials take them in the reduce).
+#define TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, OUT, ST)                             \
+  {{BM, BN, BK, WGM, WGN, OUT, ST, 1},                                           \
+   reinterpret_cast<const void *>(                                               \
+       &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST, -1, true>),              \
+   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT \
+   "_epi"}
+
+#define TBK_EPI_OUTS(BM, BN, BK, WGM, WGN, ST)                                  \
+  TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 0, ST),                                   \
+      TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 1, ST),                               \
+      TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 2, ST)

@@ -54,7 +54,10 @@ void verifyScope(Module &m, const PassOptions &) {
     for (Op &op : f.body)
       if (!allowed.count(op.name))
         throw Error("operation `" + op.name + "` is outside the stage1 scope");
-  forEachOp(m, "tb.matmul", [&](Op &op) { checkedConfig(m, op, nullptr); });
+  forEachOp(m, "tb.matmul", [&](Op &op) {
+    checkedConfig(m, op, nullptr);
+    parseEpilogueRequest(op);
+  });
 }
 
 // Reference: AttachTargetInfo.cpp:35-82.
@@ -140,7 +143,11 @@ void buildCRegister(Module &m, const PassOptions &) {
     PersistentWorkPlan pw = parsePersistentWorkPlanAttr(
         need(op, "tb.persistent_work_plan", "tb-build-program-mapping-plan"));
     AccumulatorPlan a = deriveAccumulatorPlan(c, t, e);
-    EpiloguePlan ep = deriveEpiloguePlan(c, t, e, a);
+    const EpilogueRequest req = parseEpilogueRequest(op);
+    if (!req.empty() && rd.kind == ReductionPlanKind::SplitKAtomic)
+      throw Error("fused epilogue exprs apply to the whole sum; split_k_atomic "
+                  "accumulates partial sums straight into C and cannot carry them");
+    EpiloguePlan ep = deriveEpiloguePlan(c, t, e, a, req);
     EpilogueReorderPlan ro = deriveEpilogueReorderPlan(c, a, ep);
     SharedWorkspacePlan sw = deriveSharedWorkspacePlan(c, t, e, tr, ro, rd, pw);
     WarpDecompositionPlan wd = deriveWarpDecompositionPlan(c, e, a, ep, ro, rd, pw);
@@ -316,7 +323,8 @@ void cleanupPipeline(Module &m, const PassOptions &) {
       "exact_tile", "mma", "tb.target_info", "tb.layout_plan", "tb.c_register_plan",
       "tb.mainloop_graph", "tb.schedule_plan", "tb.wait_plan", "tb.loop_plan",
       "tb.latency_plan", "tb.pipeline_plan", "tb.pipeline_expansion",
-      "tb.pipeline_ready"};
+      "tb.pipeline_ready", "epilogue_bias", "epilogue_activation",
+      "epilogue_clamp_min", "epilogue_clamp_max"};
   forEachOp(m, "tb.matmul", [&](Op &op) {
     TargetInfo t = moduleTarget(m);
     KernelConfig c = checkedConfig(m, op, &t);
@@ -409,6 +417,13 @@ void lowerToGfx950(Module &m, const PassOptions &) {
         {"group_m", I64(g.group_m)}, {"split_k", I64(g.split_k)},
         {"reduction", I64(g.reduction)}, {"num_programs", I64(g.num_programs)},
         {"xcd_remap", I64(g.xcd_remap)}};
+    if (g.epi_bias || g.epi_activation || g.epi_clamp) {
+      cfg["epi_bias"] = I64(g.epi_bias);
+      cfg["epi_activation"] = I64(g.epi_activation);
+      cfg["epi_clamp"] = I64(g.epi_clamp);
+      cfg["clamp_min"] = F32(g.clamp_min);
+      cfg["clamp_max"] = F32(g.clamp_max);
+    }
     launch.attrs["config"] = Dict(cfg);
     launch.attrs["kernel"] = Str(kernelInstanceName(g));
     launch.attrs["grid"] = Dense({g.num_programs, 1, 1});
@@ -637,6 +652,14 @@ tb_gemm_config launchConfigOf(const Op &launch) {
   g.reduction = (int32_t)getI64(c, "reduction");
   g.num_programs = getI64(c, "num_programs");
   g.xcd_remap = (int32_t)getI64(c, "xcd_remap");
+  // fused epilogue fields are printed only when some step is requested
+  if (has(c, "epi_bias")) {
+    g.epi_bias = (int32_t)getI64(c, "epi_bias");
+    g.epi_activation = (int32_t)getI64(c, "epi_activation");
+    g.epi_clamp = (int32_t)getI64(c, "epi_clamp");
+    g.clamp_min = (float)getF64(c, "clamp_min");
+    g.clamp_max = (float)getF64(c, "clamp_max");
+  }
   return g;
 }
 
@@ -650,11 +673,15 @@ std::string kernelInstanceName(const tb_gemm_config &c) {
     out = 0;
   else
     out = c.acc_init == TB_ACC_INIT_LOAD_C ? 2 : 1;
+  // fused epilogue steps run in an `_epi` instance, except on split-K
+  // partials (the reduction applies them)
+  const bool epi = (c.epi_bias || c.epi_activation || c.epi_clamp) &&
+                   c.mapping != TB_MAP_SPLIT_K;
   char buf[128];
-  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d",
+  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d%s",
            (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
            (long long)c.wave_grid_m, (long long)c.wave_grid_n, (long long)c.stages,
-           out);
+           out, epi ? "_epi" : "");
   return buf;
 }
 

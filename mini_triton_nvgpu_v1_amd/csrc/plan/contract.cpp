@@ -139,6 +139,14 @@ void verifyMainlineContract(const Module &m, const Op &op, const KernelContract 
   if (pm.persistent)
     require(k.persistentWork.residentPrograms <= k.target.numSms,
             "persistent residency exceeds the CU count");
+  // --- fused epilogue: known steps in canonical order, on a whole sum
+  const EpilogueRequest er = epilogueRequestOf(k.epilogue);
+  require(er.empty() || k.reduction.kind != ReductionPlanKind::SplitKAtomic,
+          "fused epilogue exprs cannot ride on split_k_atomic partial sums");
+  const bool hasConvert =
+      !k.epilogue.exprs.empty() && k.epilogue.exprs.back().kind == EpilogueExprKind::Convert;
+  require(hasConvert == (c.cScalar == ScalarKind::F16),
+          "an f16 C needs the f32 -> f16 convert as the last epilogue expr, an f32 C none");
   // --- resources
   require(k.sharedWorkspace.totalBytes ==
               c.requestedStages * (c.blockM + c.blockN) * c.blockK * scalarBytes(c.aScalar),
@@ -224,6 +232,16 @@ tb_gemm_config lowerContractToConfig(const KernelContract &k) {
   }
   g.num_programs = pm.persistent ? k.persistentWork.residentPrograms : pm.totalPrograms;
   g.xcd_remap = pm.xcdRemap;
+  const EpilogueRequest r = epilogueRequestOf(k.epilogue);
+  g.epi_bias = r.bias.empty() ? TB_EPI_BIAS_NONE
+                              : (r.bias == "f16" ? TB_EPI_BIAS_F16 : TB_EPI_BIAS_F32);
+  g.epi_activation = r.activation.empty()       ? TB_ACT_NONE
+                     : r.activation == "relu"   ? TB_ACT_RELU
+                     : r.activation == "silu"   ? TB_ACT_SILU
+                                                : TB_ACT_GELU_TANH;
+  g.epi_clamp = (r.hasMin ? TB_CLAMP_MIN : 0) | (r.hasMax ? TB_CLAMP_MAX : 0);
+  g.clamp_min = r.hasMin ? (float)r.clampMin : 0.0f;
+  g.clamp_max = r.hasMax ? (float)r.clampMax : 0.0f;
   return g;
 }
 

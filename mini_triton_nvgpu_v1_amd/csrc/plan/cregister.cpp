@@ -3,6 +3,9 @@
 #include "serialize.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
 
 namespace tb {
 
@@ -158,8 +161,147 @@ template <class V> void fields(V &v, EpiloguePlan &p) {
 // onto its prior contents (C += A B, the reference's semantics, init by a
 // direct vector load), an f16 C receives cast(A B) (init zero, one f32 -> f16
 // convert).
+// ---- fused epilogue exprs ------------------------------------------------------
+static const char *const kActivations[] = {"relu", "gelu_tanh", "silu"};
+
+static bool knownActivation(const std::string &s) {
+  for (const char *a : kActivations)
+    if (s == a)
+      return true;
+  return false;
+}
+
+// Clamp bounds travel in the Clamp expr's `aux` as `min=<v>,max=<v>` (either
+// part optional), each printed with enough digits to read back the f32 value.
+static std::string clampAux(const EpilogueRequest &r) {
+  char buf[96];
+  std::string s;
+  if (r.hasMin) {
+    snprintf(buf, sizeof buf, "min=%.9g", r.clampMin);
+    s += buf;
+  }
+  if (r.hasMax) {
+    snprintf(buf, sizeof buf, "%smax=%.9g", s.empty() ? "" : ",", r.clampMax);
+    s += buf;
+  }
+  return s;
+}
+
+static void checkRequest(const EpilogueRequest &r) {
+  if (!r.bias.empty() && r.bias != "f16" && r.bias != "f32")
+    throw Error("`epilogue_bias` must be \"f16\" or \"f32\", got \"" + r.bias + "\"");
+  if (!r.activation.empty() && !knownActivation(r.activation))
+    throw Error("`epilogue_activation` must be one of \"relu\", \"gelu_tanh\", "
+                "\"silu\", got \"" + r.activation + "\"");
+  if ((r.hasMin && !std::isfinite(r.clampMin)) || (r.hasMax && !std::isfinite(r.clampMax)))
+    throw Error("epilogue clamp bounds must be finite");
+  if (r.hasMin && r.hasMax && r.clampMin > r.clampMax)
+    throw Error("`epilogue_clamp_min` must not exceed `epilogue_clamp_max`");
+}
+
+EpilogueRequest parseEpilogueRequest(const Op &op) {
+  EpilogueRequest r;
+  auto str = [&](const char *name, std::string &out) {
+    auto it = op.attrs.find(name);
+    if (it == op.attrs.end())
+      return;
+    if (it->second->kind != AttrKind::String)
+      throw Error(std::string("`") + name + "` must be a string attribute");
+    out = it->second->s;
+  };
+  auto num = [&](const char *name, bool &has, double &out) {
+    auto it = op.attrs.find(name);
+    if (it == op.attrs.end())
+      return;
+    if (it->second->kind == AttrKind::Float)
+      out = it->second->f;
+    else if (it->second->kind == AttrKind::Int)
+      out = (double)it->second->i;
+    else
+      throw Error(std::string("`") + name + "` must be a float attribute");
+    out = (double)(float)out; // the kernels clamp in f32
+    has = true;
+  };
+  str("epilogue_bias", r.bias);
+  str("epilogue_activation", r.activation);
+  num("epilogue_clamp_min", r.hasMin, r.clampMin);
+  num("epilogue_clamp_max", r.hasMax, r.clampMax);
+  checkRequest(r);
+  return r;
+}
+
+EpilogueRequest epilogueRequestOf(const EpiloguePlan &p) {
+  EpilogueRequest r;
+  // canonical order: LoadBias, Add, Activation, Clamp, Convert
+  int stage = 0;
+  auto order = [&](int s, const char *what) {
+    if (s < stage)
+      throw Error(std::string("epilogue expr `") + what +
+                  "` is out of order (load_bias, add, activation, clamp, convert)");
+    stage = s;
+  };
+  bool loaded = false, added = false;
+  for (const EpilogueExprOp &x : p.exprs) {
+    switch (x.kind) {
+    case EpilogueExprKind::LoadBias:
+      order(0, "load_bias");
+      if (loaded || (x.inputScalar != ScalarKind::F16 && x.inputScalar != ScalarKind::F32))
+        throw Error("epilogue load_bias must appear once, reading f16 or f32");
+      r.bias = x.inputScalar == ScalarKind::F16 ? "f16" : "f32";
+      loaded = true;
+      break;
+    case EpilogueExprKind::Add:
+      order(1, "add");
+      if (!loaded || added || x.aux != "bias")
+        throw Error("epilogue add must follow load_bias and add the bias");
+      added = true;
+      break;
+    case EpilogueExprKind::Activation:
+      order(2, "activation");
+      if (!r.activation.empty() || !knownActivation(x.aux))
+        throw Error("epilogue activation `" + x.aux + "` is not supported on gfx950");
+      r.activation = x.aux;
+      break;
+    case EpilogueExprKind::Clamp: {
+      order(3, "clamp");
+      if (r.hasMin || r.hasMax)
+        throw Error("epilogue clamp must appear once");
+      size_t pos = 0;
+      while (pos < x.aux.size()) {
+        size_t end = x.aux.find(',', pos);
+        if (end == std::string::npos)
+          end = x.aux.size();
+        const std::string part = x.aux.substr(pos, end - pos);
+        const bool isMin = part.rfind("min=", 0) == 0, isMax = part.rfind("max=", 0) == 0;
+        if (!isMin && !isMax)
+          throw Error("epilogue clamp aux `" + x.aux + "` is not `min=<v>,max=<v>`");
+        char *stop = nullptr;
+        const double v = strtod(part.c_str() + 4, &stop);
+        if (stop == part.c_str() + 4 || *stop)
+          throw Error("epilogue clamp aux `" + x.aux + "` holds a bad number");
+        (isMin ? r.hasMin : r.hasMax) = true;
+        (isMin ? r.clampMin : r.clampMax) = v;
+        pos = end + 1;
+      }
+      if (!r.hasMin && !r.hasMax)
+        throw Error("epilogue clamp names neither bound");
+      break;
+    }
+    case EpilogueExprKind::Convert:
+      order(4, "convert");
+      break;
+    }
+  }
+  if (loaded != added)
+    throw Error("epilogue load_bias and add come as a pair");
+  checkRequest(r);
+  return r;
+}
+
 EpiloguePlan deriveEpiloguePlan(const KernelConfig &c, const TargetInfo &,
-                                const EncodingPlan &e, const AccumulatorPlan &a) {
+                                const EncodingPlan &e, const AccumulatorPlan &a,
+                                const EpilogueRequest &req) {
+  checkRequest(req);
   WaveGeom g = waveGeom(c, e);
   bool boundary = c.problemM % c.blockM != 0 || c.problemN % c.blockN != 0;
   DirectGlobalVectorPlan dv;
@@ -182,6 +324,27 @@ EpiloguePlan deriveEpiloguePlan(const KernelConfig &c, const TargetInfo &,
     p.initMode = AccumulatorInitMode::Zero;
     p.init.present = false;
     p.init.ownerScope = "none";
+  }
+  // fused steps on the f32 accumulator, 4 columns per lane at a time
+  auto expr = [&](EpilogueExprKind k, ScalarKind in, const std::string &aux) {
+    EpilogueExprOp x;
+    x.kind = k;
+    x.inputScalar = in;
+    x.outputScalar = ScalarKind::F32;
+    x.vectorWidth = 4;
+    x.aux = aux;
+    p.exprs.push_back(x);
+  };
+  if (!req.bias.empty()) {
+    expr(EpilogueExprKind::LoadBias,
+         req.bias == "f16" ? ScalarKind::F16 : ScalarKind::F32, "bias");
+    expr(EpilogueExprKind::Add, ScalarKind::F32, "bias");
+  }
+  if (!req.activation.empty())
+    expr(EpilogueExprKind::Activation, ScalarKind::F32, req.activation);
+  if (req.hasMin || req.hasMax)
+    expr(EpilogueExprKind::Clamp, ScalarKind::F32, clampAux(req));
+  if (c.cScalar != ScalarKind::F32) {
     EpilogueExprOp cvt;
     cvt.kind = EpilogueExprKind::Convert;
     cvt.inputScalar = ScalarKind::F32;

@@ -296,8 +296,29 @@ struct EpiloguePlan {
   TargetLandingPlan targetLanding;
   std::vector<EpilogueExprOp> exprs;
 };
+// Fused epilogue steps requested on tb.matmul through the optional attrs
+// `epilogue_bias` ("f16" | "f32": a length-N vector added to every row),
+// `epilogue_activation` ("relu" | "gelu_tanh" | "silu"), `epilogue_clamp_min`
+// and `epilogue_clamp_max` (f32). The reference declares the expr kinds
+// (include/tb/Analysis/EpiloguePlan.h:61-75, serialized at
+// lib/Analysis/EpiloguePlan.cpp:423-459) but never derives them and gives
+// tb.matmul no way to ask for them; these attrs are that surface. The steps
+// always apply in the order bias, activation, clamp, then the C conversion.
+struct EpilogueRequest {
+  std::string bias;       // "", "f16" or "f32"
+  std::string activation; // "", "relu", "gelu_tanh" or "silu"
+  bool hasMin = false, hasMax = false;
+  double clampMin = 0.0, clampMax = 0.0;
+  bool empty() const { return bias.empty() && activation.empty() && !hasMin && !hasMax; }
+};
+// From the tb.matmul attrs (validated; an op without them gives an empty request).
+EpilogueRequest parseEpilogueRequest(const Op &matmul);
+// Back from a derived plan's exprs (validated: canonical order, known kinds).
+EpilogueRequest epilogueRequestOf(const EpiloguePlan &p);
+
 EpiloguePlan deriveEpiloguePlan(const KernelConfig &c, const TargetInfo &t,
-                                const EncodingPlan &e, const AccumulatorPlan &a);
+                                const EncodingPlan &e, const AccumulatorPlan &a,
+                                const EpilogueRequest &req = {});
 AttrP buildEpiloguePlanAttr(const EpiloguePlan &p);
 EpiloguePlan parseEpiloguePlanAttr(const Attr &a);
 

@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <limits>
@@ -67,6 +68,22 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
     return fail("wave grid must multiply to num_waves");
   if (c.split_k < 1)
     return fail("split_k must be >= 1");
+  if (c.epi_bias < TB_EPI_BIAS_NONE || c.epi_bias > TB_EPI_BIAS_F32)
+    return fail("epi_bias must be TB_EPI_BIAS_NONE, _F16 or _F32");
+  if (c.epi_activation < TB_ACT_NONE || c.epi_activation > TB_ACT_SILU)
+    return fail("epi_activation must be TB_ACT_NONE, _RELU, _GELU_TANH or _SILU");
+  if (c.epi_clamp & ~(TB_CLAMP_MIN | TB_CLAMP_MAX))
+    return fail("epi_clamp holds unknown bits");
+  if (((c.epi_clamp & TB_CLAMP_MIN) && !std::isfinite(c.clamp_min)) ||
+      ((c.epi_clamp & TB_CLAMP_MAX) && !std::isfinite(c.clamp_max)))
+    return fail("clamp bounds must be finite");
+  if ((c.epi_clamp & TB_CLAMP_MIN) && (c.epi_clamp & TB_CLAMP_MAX) &&
+      c.clamp_min > c.clamp_max)
+    return fail("clamp_min must not exceed clamp_max");
+  const bool fused = c.epi_bias || c.epi_activation || c.epi_clamp;
+  if (fused && c.reduction == TB_RED_ATOMIC)
+    return fail("fused epilogue steps need the whole sum; atomic split-K "
+                "accumulates partial sums into C");
   if (c.group_m < 1)
     return fail("group_m must be >= 1");
   const int64_t tiles_m = ceil_div(c.m, c.block_m);
@@ -125,18 +142,20 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
   if (total_work > std::numeric_limits<int>::max())
     return fail("too many programs");
 
+  // split-K partials take the fused steps in the reduction instead
+  const int epi = fused && c.mapping != TB_MAP_SPLIT_K ? 1 : 0;
   tbk::KernelKey key{(int)c.block_m, (int)c.block_n, (int)c.block_k,
                      (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode,
-                     (int)c.stages};
+                     (int)c.stages, epi};
   const tbk::KernelEntry *e = tbk::find_kernel(key);
   if (!e) {
     char buf[256];
     snprintf(buf, sizeof buf,
              "no gfx950 kernel instance for tile %lldx%lldx%lld, wave grid "
-             "%lldx%lld, %lld LDS stages, output mode %d",
+             "%lldx%lld, %lld LDS stages, output mode %d%s",
              (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
              (long long)c.wave_grid_m, (long long)c.wave_grid_n,
-             (long long)c.stages, out_mode);
+             (long long)c.stages, out_mode, epi ? " with fused epilogue steps" : "");
     return fail(buf);
   }
   tb_gemm_desc *d = new tb_gemm_desc();
@@ -193,10 +212,29 @@ void tb_desc_free(tb_gemm_desc *desc) { delete desc; }
 
 int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
                    void *c, void *workspace, void *stream) {
+  if (d && d->cfg.epi_bias != TB_EPI_BIAS_NONE)
+    return fail("tb_gemm_launch: this descriptor adds a bias; pass it through "
+                "tb_gemm_launch_ex");
+  return tb_gemm_launch_ex(d, a, b, c, nullptr, workspace, stream);
+}
+
+int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
+                      void *c, const void *bias, void *workspace, void *stream) {
   if (!d)
     return fail("tb_gemm_launch: desc is NULL");
   if (!a || !b || !c)
     return fail("tb_gemm_launch: A, B and C must be device pointers");
+  if (d->cfg.epi_bias != TB_EPI_BIAS_NONE) {
+    // the epilogue reads 4 bias values per vector load
+    const uintptr_t align = d->cfg.epi_bias == TB_EPI_BIAS_F16 ? 8 : 16;
+    if (!bias)
+      return fail("tb_gemm_launch_ex: this descriptor adds a bias; bias is NULL");
+    if (reinterpret_cast<uintptr_t>(bias) % align)
+      return fail("tb_gemm_launch_ex: the bias must be " + std::to_string(align) +
+                  "-byte aligned");
+  } else if (bias) {
+    return fail("tb_gemm_launch_ex: this descriptor has no bias step; pass NULL");
+  }
   if (d->workspace_bytes && !workspace)
     return fail("tb_gemm_launch: this descriptor needs a workspace of " +
                 std::to_string(d->workspace_bytes) + " bytes");
@@ -221,6 +259,12 @@ int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
   p.total_work = (int)d->total_work;
   p.xcds = cf.xcd_remap;
   p.ws_ld = (int)cf.n;
+  p.bias = bias;
+  p.epi_bias = cf.epi_bias;
+  p.epi_act = cf.epi_activation;
+  p.epi_clamp = cf.epi_clamp;
+  p.clamp_lo = cf.clamp_min;
+  p.clamp_hi = cf.clamp_max;
   if (d->out_mode == tbk::kOutF32Partial && cf.mapping != TB_MAP_SPLIT_K) {
     p.ws = reinterpret_cast<float *>(c); // plain f32 store into C
     p.ws_ld = (int)cf.ldc;
@@ -235,7 +279,11 @@ int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
     if (int rc = check_hip(
             tbk::launch_reduce_ex(p.ws, c, p.M, p.N, p.ldc, p.split_k,
                                   cf.c_dtype == TB_DTYPE_F16 ? 1 : 0,
-                                  cf.acc_init == TB_ACC_INIT_LOAD_C ? 1 : 0, s),
+                                  cf.acc_init == TB_ACC_INIT_LOAD_C ? 1 : 0,
+                                  tbk::EpiArgs{bias, cf.epi_bias, cf.epi_activation,
+                                               cf.epi_clamp, cf.clamp_min,
+                                               cf.clamp_max},
+                                  s),
             "hipLaunchKernel(split-k reduce)"))
       return rc;
   }

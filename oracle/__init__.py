@@ -62,6 +62,9 @@ def lib() -> ctypes.CDLL:
         L.tbo_check_tolerance.restype = i64
         L.tbo_gemm_f32.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_int]
         L.tbo_gemm_f32.restype = None
+        L.tbo_epilogue_f64.argtypes = [vp, i64, i64, i64, vp, ctypes.c_int,
+                                       ctypes.c_int, dbl, dbl]
+        L.tbo_epilogue_f64.restype = None
         L.tbo_max_threads.argtypes = []
         L.tbo_max_threads.restype = ctypes.c_int
         L.tbo_program_to_tile.argtypes = [ctypes.c_int, i64, i64, i64, i64, i64,
@@ -128,6 +131,22 @@ def gemm_f64(A: np.ndarray, B: np.ndarray, init: np.ndarray | None = None,
         ldi = N
     lib().tbo_gemm_f64(_ptr(A), _ptr(B), init_ptr, _ptr(ref), M, N, K, K, N,
                        ldi, N, row_begin, row_end, threads)
+    return ref
+
+
+def epilogue_f64(ref: np.ndarray, bias: np.ndarray | None = None, act: int = 0,
+                 clamp_bits: int = 0, lo: float = 0.0, hi: float = 0.0) -> np.ndarray:
+    """Fused epilogue steps applied in place to an f64 result (bias, then
+    activation 0 none / 1 relu / 2 gelu_tanh / 3 silu, then clamp)."""
+    assert ref.dtype == np.float64 and ref.flags.c_contiguous
+    rows, N = ref.shape
+    bias_ptr = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.float64)
+        assert bias.shape == (N,)
+        bias_ptr = _ptr(bias)
+    lib().tbo_epilogue_f64(_ptr(ref), rows, N, N, bias_ptr, act, clamp_bits,
+                           float(lo), float(hi))
     return ref
 
 

@@ -180,6 +180,38 @@ void tbo_gemm_f64(const uint16_t *A, const uint16_t *B, const float *init,
   free(Bd);
 }
 
+/* ------------------------------------------------------------------------ */
+/* Fused epilogue steps on an f64 result, in place: ref[r][c] += bias[c],
+ * then the activation, then the clamp (the order the backend derives; the
+ * reference declares these expr kinds, include/tb/Analysis/EpiloguePlan.h:
+ * 61-75, but implements none, so the formulas are the textbook ones:
+ * relu max(x, 0); GELU in its tanh form, Hendrycks & Gimpel 2016,
+ * 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); SiLU x / (1 + e^-x)).
+ * act: 0 none, 1 relu, 2 gelu_tanh, 3 silu. clamp_bits: 1 min, 2 max.      */
+/* ------------------------------------------------------------------------ */
+void tbo_epilogue_f64(double *ref, int64_t rows, int64_t N, int64_t ldr,
+                      const double *bias, int act, int clamp_bits, double lo,
+                      double hi) {
+  const double k0 = sqrt(2.0 / 3.14159265358979323846);
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t j = 0; j < N; ++j) {
+      double x = ref[r * ldr + j];
+      if (bias)
+        x += bias[j];
+      if (act == 1)
+        x = x > 0.0 ? x : 0.0;
+      else if (act == 2)
+        x = 0.5 * x * (1.0 + tanh(k0 * (x + 0.044715 * x * x * x)));
+      else if (act == 3)
+        x = x / (1.0 + exp(-x));
+      if ((clamp_bits & 1) && x < lo)
+        x = lo;
+      if ((clamp_bits & 2) && x > hi)
+        x = hi;
+      ref[r * ldr + j] = x;
+    }
+}
+
 int64_t tbo_check_tolerance(const void *got, int got_is_f32, int64_t ldg,
                             const double *ref, int64_t ldr, int64_t N,
                             int64_t row_begin, int64_t row_end, double rtol,

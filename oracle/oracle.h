@@ -51,6 +51,12 @@ void tbo_gemm_f64(const uint16_t *A, const uint16_t *B, const float *init,
  * (got_is_f32 = 0) or f32 (got_is_f32 = 1) with leading dimension ldg; ref as
  * produced by tbo_gemm_f64 for rows [row_begin, row_end). Returns the number
  * of violations; writes the largest |got-ref| and its (row, col). */
+/* Fused epilogue steps in place on an f64 result (rows x N, leading
+ * dimension ldr): += bias[c] (bias may be NULL), activation (0 none, 1 relu,
+ * 2 gelu_tanh, 3 silu), clamp (bit 1: max(x, lo), bit 2: min(x, hi)). */
+void tbo_epilogue_f64(double *ref, int64_t rows, int64_t N, int64_t ldr,
+                      const double *bias, int act, int clamp_bits, double lo,
+                      double hi);
 int64_t tbo_check_tolerance(const void *got, int got_is_f32, int64_t ldg,
                             const double *ref, int64_t ldr, int64_t N,
                             int64_t row_begin, int64_t row_end, double rtol,

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirror of tb_gemm_config matches the C compiler's layout."""
-    assert tb.lib().tb_abi_version() == 1
+    assert tb.lib().tb_abi_version() == 2
     fields = [name for name, _ in tb.GemmConfig._fields_]
     src = tmp_path / "layout.c"
     src.write_text(
@@ -85,6 +85,15 @@ def _cfg(**kw):
     (dict(acc_init=tb.ACC_INIT_LOAD_C), "f32 C"),
     (dict(num_programs=7), "launch formula"),
     (dict(mapping=9), "unknown mapping"),
+    (dict(epi_bias=3), "epi_bias"),
+    (dict(epi_activation=4), "epi_activation"),
+    (dict(epi_clamp=4), "unknown bits"),
+    (dict(epi_clamp=tb.CLAMP_MIN, clamp_min=float("inf")), "finite"),
+    (dict(epi_clamp=tb.CLAMP_MIN | tb.CLAMP_MAX, clamp_min=1.0, clamp_max=0.0),
+     "must not exceed"),
+    (dict(epi_activation=tb.ACT_RELU, c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_LOAD_C,
+          mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_ATOMIC, num_programs=2),
+     "whole sum"),
 ])
 def test_descriptor_validation_errors(kw, msg):
     with pytest.raises(tb.TbError, match=msg):
@@ -97,3 +106,25 @@ def test_launch_argument_errors_before_any_gpu_call():
         d.launch(0, 0, 0)
     with pytest.raises(tb.TbError, match="workspace"):
         d.launch(16, 16, 16, None)
+
+
+def test_fused_epilogue_instances_and_bias_arguments():
+    """A fused config binds an `_epi` instance (split-K keeps the plain GEMM
+    instance and fuses the steps into its reduction); the bias pointer is
+    required exactly when the config adds one, and must be vector-aligned."""
+    d = tb.GemmDesc.from_config(_cfg(epi_activation=tb.ACT_RELU))
+    assert d.kernel_name.endswith("_epi")
+    sk = configs.SPLIT_K.direct_config()
+    sk.epi_bias = tb.EPI_BIAS_F32
+    assert not tb.GemmDesc.from_config(sk).kernel_name.endswith("_epi")
+    plain = tb.GemmDesc.from_config(_cfg())
+    assert not plain.kernel_name.endswith("_epi")
+    with pytest.raises(tb.TbError, match="no bias step"):
+        plain.launch(16, 16, 16, bias=256)
+    biased = tb.GemmDesc.from_config(_cfg(epi_bias=tb.EPI_BIAS_F32))
+    with pytest.raises(tb.TbError, match="tb_gemm_launch_ex"):
+        biased.launch(16, 16, 16)
+    with pytest.raises(tb.TbError, match="16-byte aligned"):
+        biased.launch(16, 16, 16, bias=260)
+    with pytest.raises(tb.TbError, match="device pointers"):
+        biased.launch(0, 0, 0, bias=256)

@@ -139,20 +139,28 @@ def test_ragged_edges(M, N, K, tile, device):
 def _every_instance():
     seen = set()
     for name in tb.kernel_names():
-        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{STAGES}_out{OUT}
+        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{STAGES}_out{OUT}[_epi]
         body = name[len("tb_gemm_gfx950_"):]
-        shape, waves, stages, out = body.split("_")
+        epi = body.endswith("_epi")
+        shape, waves, stages, out = body[:-4 if epi else None].split("_")
         bm, bn, bk = map(int, shape.split("x"))
         wgm, wgn = map(int, waves[1:].split("x"))
-        seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:])))
+        seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:]), int(epi)))
     return sorted(seen)
+
+
+# fused steps per output mode of the `_epi` instances: (bias kind, activation,
+# clamp bits, lo, hi)
+EPI_STEPS = {0: (tb.EPI_BIAS_F16, tb.ACT_GELU_TANH, 3, -0.5, 1.5),
+             1: (tb.EPI_BIAS_F32, tb.ACT_SILU, 0, 0.0, 0.0),
+             2: (tb.EPI_BIAS_F32, tb.ACT_RELU, 2, 0.0, 2.0)}
 
 
 @pytest.mark.parametrize("inst", _every_instance(), ids=lambda t: "x".join(map(str, t)))
 def test_every_instance(inst, device):
     """Each compiled instance on a shape with several K tiles (more than the
     stage count, plus a ragged last tile when possible) and an M/N edge."""
-    bm, bn, bk, wgm, wgn, stages, out = inst
+    bm, bn, bk, wgm, wgn, stages, out, epi = inst
     M, N, K = bm + 40, bn * 2 - 24, bk * 5 + (bk // 2 if out == 0 else 0)
     print(f"instance {inst} on {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0200 + bm + bn + bk, oracle.UNIFORM)
@@ -167,6 +175,11 @@ def test_every_instance(inst, device):
                             mapping=tb.MAP_GROUPED_TILE, split_k=1,
                             reduction=tb.RED_NONE, num_programs=tm * tn, **kw)
         c_dtype = torch.float16
+    elif out == 1 and epi:  # plain f32 store (only fused instances are bound)
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_ZERO,
+                            mapping=tb.MAP_TILE, split_k=1, reduction=tb.RED_NONE,
+                            num_programs=tm * tn, **kw)
+        c_dtype = torch.float32
     elif out == 1:  # f32 partials: split-K with workspace, f16 result
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO,
                             mapping=tb.MAP_SPLIT_K, split_k=3,
@@ -185,9 +198,30 @@ def test_every_instance(inst, device):
                             mapping=tb.MAP_SPLIT_K, split_k=2,
                             reduction=tb.RED_ATOMIC, num_programs=tm * tn * 2, **kw)
         c_dtype = torch.float32
+    if not epi:
+        desc = tb.GemmDesc.from_config(cfg)
+        got = run_desc(desc, A, B, device, c_init=init, c_dtype=c_dtype)
+        check(got, A, B, init=init)
+        return
+    kind, act, bits, lo, hi = EPI_STEPS[out]
+    cfg.epi_bias, cfg.epi_activation, cfg.epi_clamp = kind, act, bits
+    cfg.clamp_min, cfg.clamp_max = lo, hi
     desc = tb.GemmDesc.from_config(cfg)
-    got = run_desc(desc, A, B, device, c_init=init, c_dtype=c_dtype)
-    check(got, A, B, init=init)
+    assert desc.kernel_name.endswith(f"_out{out}_epi")
+    bias = oracle.fill_f16(1, N, 0x5EED0300 + N, oracle.UNIFORM, 1.0).reshape(N)
+    if kind == tb.EPI_BIAS_F32:
+        bias = bias.astype(np.float32)
+    dA, dB = _dev(A, device), _dev(B, device)
+    dC = (_dev(init, device) if init is not None else
+          torch.full((M, N), float("nan"), dtype=c_dtype, device=device))
+    desc.launch(dA, dB, dC, bias=_dev(bias, device))
+    torch.cuda.synchronize()
+    got = dC.cpu().numpy()
+    ref = oracle.gemm_f64(A, B, init=init)
+    oracle.epilogue_f64(ref, bias.astype(np.float64), act, bits, lo, hi)
+    bad, err, worst = oracle.check_tolerance(got, ref, rtol=RTOL)
+    print(f"fused steps: violations={bad} max|err|={err:.3e}", flush=True)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
 
 
 @pytest.mark.parametrize("mapping", [tb.MAP_PERSISTENT_TILE, tb.MAP_PERSISTENT_GROUPED])

@@ -172,6 +172,58 @@ def test_planted_oracle_mistake_is_caught():
     assert oracle.check_tolerance(dropped.astype(np.float32), good, rtol=1e-6)[0] > 0
 
 
+# ---- fused epilogue steps ----------------------------------------------------
+def _epi(x, **kw):
+    r = np.array(x, dtype=np.float64).reshape(1, -1).copy()
+    return oracle.epilogue_f64(r, **kw)[0]
+
+
+def test_epilogue_activations_match_torch_cpu():
+    """GELU (tanh form) and SiLU against torch's own CPU implementations in
+    f64, an independent code path; relu against the definition."""
+    import torch
+    x = np.linspace(-8.0, 8.0, 1601)
+    t = torch.from_numpy(x)
+    gelu = torch.nn.functional.gelu(t, approximate="tanh").numpy()
+    silu = torch.nn.functional.silu(t).numpy()
+    assert np.allclose(_epi(x, act=2), gelu, rtol=0, atol=1e-13)
+    assert np.allclose(_epi(x, act=3), silu, rtol=0, atol=1e-13)
+    assert np.array_equal(_epi(x, act=1), np.where(x > 0, x, 0.0))
+    assert np.array_equal(_epi(x, act=0), x)
+
+
+def test_epilogue_closed_forms_and_symmetry():
+    """f(0) = 0; f(x) - f(-x) = x for GELU-tanh and SiLU (their gates g
+    satisfy g(x) + g(-x) = 1); f(x) -> x for large x and -> 0 for very
+    negative x. A sign error in a term breaks the symmetry."""
+    x = np.linspace(0.01, 6.0, 300)
+    for act in (2, 3):
+        assert _epi([0.0], act=act)[0] == 0.0
+        assert np.allclose(_epi(x, act=act) - _epi(-x, act=act), x, atol=1e-12)
+        assert abs(_epi([40.0], act=act)[0] - 40.0) < 1e-12
+        assert abs(_epi([-40.0], act=act)[0]) < 1e-12
+    # known values (tanh-GELU at 1: 0.5 (1 + tanh(sqrt(2/pi) 1.044715)))
+    assert abs(_epi([1.0], act=2)[0] - 0.8411919906082768) < 1e-12
+    assert abs(_epi([1.0], act=3)[0] - 1.0 / (1.0 + math.exp(-1.0))) < 1e-15
+
+
+def test_epilogue_order_bias_activation_clamp():
+    """bias before the activation, clamp last: each order mistake (planted
+    here by composing the steps differently) gives a different answer."""
+    bias = np.array([0.5, -2.0, 1.0])
+    x = np.array([-1.0, 1.5, -3.0])
+    got = _epi(x, bias=bias, act=3, clamp_bits=3, lo=-0.2, hi=0.4)
+    z = x + bias
+    expect = np.clip(z / (1 + np.exp(-z)), -0.2, 0.4)
+    assert np.allclose(got, expect, atol=1e-15)
+    act_first = np.clip(x / (1 + np.exp(-x)) + bias, -0.2, 0.4)
+    clamp_first = (lambda c: c / (1 + np.exp(-c)))(np.clip(z, -0.2, 0.4))
+    assert not np.allclose(got, act_first) and not np.allclose(got, clamp_first)
+    # one-sided clamps
+    assert np.array_equal(_epi([-5.0, 5.0], clamp_bits=1, lo=-1.0), [-1.0, 5.0])
+    assert np.array_equal(_epi([-5.0, 5.0], clamp_bits=2, hi=1.0), [-5.0, 1.0])
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (13, 37, 29), (130, 70, 300)])
 def test_gemm_f32_baseline_matches_numpy(M, N, K):
     rng = np.random.default_rng(K)
