@@ -274,6 +274,33 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int j = 0; j < TN; ++j)
         acc[i][j] = (f32x16){};
 
+    // C += A*B on small wave tiles of 4-wave workgroups (512 registers per
+    // lane): the prior C is loaded before the tile's first A/B loads, so its
+    // latency overlaps the main loop instead of following it. Issued first,
+    // these loads are older than every A/B load, so the main loop's vmcnt
+    // waits stay as they are.
+    constexpr bool PREFETCH_C = OUT == kOutF32Accum && TM * TN <= 4 && NW <= 4;
+    f32x4 c_pre[PREFETCH_C ? TM : 1][PREFETCH_C ? TN : 1][4];
+    if constexpr (PREFETCH_C) {
+      const __amdgpu_buffer_rsrc_t rc =
+          make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 4u);
+      const int row0 = m0 + wm * T::WTM + (lane & 31);
+      const int col0 = n0 + wn * T::WTN + 4 * khalf;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int row = row0 + i * 32, col = col0 + j * 32 + 8 * g;
+            const uint32_t off = (row < p.M && col < p.N)
+                                     ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 4u
+                                     : kOob;
+            c_pre[i][j][g] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
+          }
+    }
+
     // The k-dependent part of each global address is wave-uniform and rides
     // in the scalar offset; a row, column or k range outside the problem gets
     // the vector offset kOob, which loads zero.
@@ -605,35 +632,56 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       const int ld = OUT == kOutF32Partial ? p.ws_ld : p.ldc;
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+      auto c_off = [&](int i, int j, int g) -> uint32_t {
+        const int row = crow_base + i * 32, col = ccol_base + j * 32 + 8 * g;
+        return (row < p.M && col < p.N)
+                   ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                   : kOob;
+      };
+      // C += A*B reads the prior C first. All loads of a group of tiles (the
+      // whole wave tile when it holds at most 4 MFMA tiles, else one row of
+      // tiles) are issued before the first add, so the group waits for
+      // memory once rather than once per tile.
+      constexpr int GI = TM * TN <= 4 ? TM : 1; // tile rows per group
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = crow_base + i * 32;
+      for (int i0 = 0; i0 < TM; i0 += GI) {
+        f32x4 old[GI][TN][4];
+        if constexpr (OUT == kOutF32Accum && !PREFETCH_C) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
+          for (int ii = 0; ii < GI; ++ii)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int col = ccol_base + j * 32 + 8 * g;
-            const bool ok = row < p.M && col < p.N;
-            const uint32_t off =
-                ok ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u : kOob;
-            f32x4 v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
-                       acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-            if constexpr (OUT == kOutF32Accum) {
-              const f32x4 old = __builtin_bit_cast(
-                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
-              v += old;
-              if constexpr (EPI) {
-                const epi_f32x4 b = epi_load_bias(ea, col, p.N);
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  v[r] = epi_apply1(v[r], b[r], ea);
-              }
-            }
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v),
-                                                   rc, off, 0, 0);
-          }
-          __builtin_amdgcn_sched_barrier(0); // one 32x32 tile at a time
+              for (int g = 0; g < 4; ++g)
+                old[ii][j][g] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, c_off(i0 + ii, j, g),
+                                                                 0, 0));
         }
+#pragma unroll
+        for (int ii = 0; ii < GI; ++ii)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int i = i0 + ii;
+              f32x4 v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
+                         acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+              if constexpr (OUT == kOutF32Accum) {
+                if constexpr (PREFETCH_C)
+                  v += c_pre[i][j][g];
+                else
+                  v += old[ii][j][g];
+                if constexpr (EPI) {
+                  const epi_f32x4 b = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
+#pragma unroll
+                  for (int r = 0; r < 4; ++r)
+                    v[r] = epi_apply1(v[r], b[r], ea);
+                }
+              }
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc,
+                                                     c_off(i, j, g), 0, 0);
+            }
+        __builtin_amdgcn_sched_barrier(0); // one group at a time
       }
     } else { // kOutF32Atomic
       float *C = reinterpret_cast<float *>(p.C);

@@ -18,7 +18,8 @@
       X(128, 128, 64, 2, 2, 2), X(128, 128, 64, 2, 2, 3),                       \
       X(128, 128, 64, 2, 2, 4), X(128, 64, 64, 2, 2, 2), X(128, 64, 64, 2, 2, 3), \
       X(64, 128, 64, 2, 2, 2), X(64, 128, 64, 2, 2, 3), X(128, 64, 64, 4, 1, 2), \
-      X(128, 64, 64, 4, 1, 3), X(64, 128, 64, 1, 4, 2), X(64, 128, 64, 1, 4, 3)
+      X(128, 64, 64, 4, 1, 3), X(64, 128, 64, 1, 4, 2), X(64, 128, 64, 1, 4, 3), \
+      X(128, 64, 32, 4, 1, 2), X(64, 128, 32, 1, 4, 2)
 
 // 256-wide macro-tiles (the MFMA-bound configs). 8 waves (2 per SIMD: one
 // wave's MFMAs run while the other waits) in the grid the plan derives for
