@@ -155,8 +155,9 @@ class Workload:
             split_k=self.split_k,
             reduction=RED_WORKSPACE if self.split_k > 1 else RED_NONE,
             num_programs=programs,
-            # XCD-aware program order once the tiles outnumber the 256 CUs
-            xcd_remap=8 if tiles_m * tiles_n > 256 else 0,
+            # XCD-aware program order once the tiles fill the 256 CUs
+            # (not for split-K: there each XCD holds one split's K range)
+            xcd_remap=8 if tiles_m * tiles_n >= 256 and mapping != MAP_SPLIT_K else 0,
             epi_bias=BIAS_KINDS[self.bias],
             epi_activation=ACTIVATIONS[self.activation],
             epi_clamp=(CLAMP_MIN if self.clamp_min is not None else 0)

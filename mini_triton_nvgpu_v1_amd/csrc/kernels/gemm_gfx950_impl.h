@@ -172,6 +172,19 @@ struct GemmTile {
   static constexpr bool STAGED_F16_EPILOGUE =
       SLOTTED && (WTN == 64 || WTN == 128) && WTM * WTN <= 8192 &&
       NW * WTM * EPI_ROWB <= LDS_BYTES;
+  // f32 C (C += A*B, plain f32 stores, split-K partials) staged through LDS
+  // one 32-row block of the wave tile at a time (F32_ROWB bytes per row):
+  // the accumulators go in as 16-byte pieces, come back as whole row
+  // segments, and the prior C is read and the result written in full rows.
+  // Chunk c of row r sits at c ^ ((r / F32_RPP) % F32_XOR), so the 16 lanes
+  // an LDS cycle serves touch 16 different 16-byte bank groups both ways.
+  static constexpr int F32_ROWB = WTN * 4;
+  static constexpr int F32_CPR = WTN / 4;                  // 16-byte chunks per row
+  static constexpr int F32_RPP = F32_ROWB >= 256 ? 1 : 256 / F32_ROWB;
+  static constexpr int F32_XOR = F32_CPR < 16 ? F32_CPR : 16;
+  static constexpr int F32_RPI = 64 / F32_CPR;             // rows per 64-lane read
+  static constexpr bool STAGED_F32_EPILOGUE =
+      (WTN == 32 || WTN == 64 || WTN == 128) && NW * 32 * F32_ROWB <= LDS_BYTES;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
@@ -279,7 +292,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // latency overlaps the main loop instead of following it. Issued first,
     // these loads are older than every A/B load, so the main loop's vmcnt
     // waits stay as they are.
-    constexpr bool PREFETCH_C = OUT == kOutF32Accum && TM * TN <= 4 && NW <= 4;
+    constexpr bool PREFETCH_C = OUT == kOutF32Accum && !T::STAGED_F32_EPILOGUE &&
+                                TM * TN <= 4 && NW <= 4;
     f32x4 c_pre[PREFETCH_C ? TM : 1][PREFETCH_C ? TN : 1][4];
     if constexpr (PREFETCH_C) {
       const __amdgpu_buffer_rsrc_t rc =
@@ -623,6 +637,72 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           // one 32x32 tile at a time: the conversions read the accumulators
           // through VGPRs, and letting them run ahead needs a VGPR each
           __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else if constexpr ((OUT == kOutF32Partial || OUT == kOutF32Accum) &&
+                         T::STAGED_F32_EPILOGUE) {
+      // f32 C through LDS, one 32-row block of the wave tile at a time: the
+      // prior C (C += A*B) is read and the result written as whole row
+      // segments (F32_CPR lanes x 16 bytes per row) instead of 16-byte
+      // pieces of 32 rows.
+      float *base = OUT == kOutF32Partial
+                        ? p.ws + (size_t)part * (size_t)p.M * (size_t)p.ws_ld
+                        : reinterpret_cast<float *>(p.C);
+      const int ld = OUT == kOutF32Partial ? p.ws_ld : p.ldc;
+      const __amdgpu_buffer_rsrc_t rc =
+          make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+      __syncthreads(); // every wave drained its loads and finished its reads
+      TBK_LDS char *wl =
+          (TBK_LDS char *)(TBK_LDS void *)lds + wave * (32 * T::F32_ROWB);
+      constexpr int NLD = 32 / T::F32_RPI; // row segments per lane per block
+      const int q = lane % T::F32_CPR;
+      const int col = n0 + wn * T::WTN + 4 * q;
+      const int rw = lane & 31;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row0 = m0 + wm * T::WTM + i * 32;
+        uint32_t off[NLD];
+#pragma unroll
+        for (int t = 0; t < NLD; ++t) {
+          const int row = row0 + t * T::F32_RPI + lane / T::F32_CPR;
+          off[t] = (row < p.M && col < p.N)
+                       ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                       : kOob;
+        }
+        f32x4 old[OUT == kOutF32Accum ? NLD : 1];
+        if constexpr (OUT == kOutF32Accum) {
+#pragma unroll
+          for (int t = 0; t < NLD; ++t)
+            old[t] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off[t], 0, 0));
+        }
+        // accumulators in: lane l holds row l % 32, columns 32j + 8g + 4(l / 32)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int cs = (8 * j + 2 * g + khalf) ^ ((rw / T::F32_RPP) % T::F32_XOR);
+            *(TBK_LDS f32x4 *)(wl + rw * T::F32_ROWB + cs * 16) =
+                (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
+                        acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          }
+        // whole row segments out
+#pragma unroll
+        for (int t = 0; t < NLD; ++t) {
+          const int r = t * T::F32_RPI + lane / T::F32_CPR;
+          const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
+          f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
+          if constexpr (OUT == kOutF32Accum) {
+            v += old[t];
+            if constexpr (EPI) {
+              const epi_f32x4 b = epi_load_bias(ea, col, p.N);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                v[e] = epi_apply1(v[e], b[e], ea);
+            }
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
+                                                 0, 0);
         }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {

@@ -172,7 +172,14 @@ ProgramMappingPlan deriveProgramMappingPlan(const Module &m, const KernelConfig 
   p.ctasPerCGA = {p.numCTAs, 1, 1};
   p.ctaSplitNum = {1, 1, 1};
   p.ctaOrder = {0, 1, 2};
-  p.xcdRemap = tiles > t.numSms && t.numXcds > 1 ? t.numXcds : 0;
+  // XCD-aware program order once the output tiles fill the CUs: each XCD
+  // (own L2) then works a compact block of tiles instead of every 8th one
+  // (4096^3 on 256 tiles: ~0.7% faster). Split-K keeps the plain order, in
+  // which each XCD holds one split's K range of A and B.
+  p.xcdRemap = tiles >= t.numSms && t.numXcds > 1 &&
+                       p.mappingKind != ProgramMappingKind::SplitK
+                   ? t.numXcds
+                   : 0;
   validateProgramMappingPlan(p);
   return p;
 }

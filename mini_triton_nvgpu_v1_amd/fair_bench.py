@@ -216,47 +216,59 @@ def order_cases(cases: list[FairCase], mode: str) -> list[FairCase]:
 
 
 # ---- GPU state (rocm-smi) ----------------------------------------------------
+def _smi_json(*flags) -> dict:
+    out = subprocess.run(["rocm-smi", *flags, "--json"], capture_output=True, text=True,
+                         timeout=30).stdout
+    start = out.find("{")
+    return next(iter(json.loads(out[start:]).values())) if start >= 0 else {}
+
+
 def query_gpu_state() -> dict[str, Any]:
-    """Current/max shader clock, memory clock and edge temperature of GPU 0;
-    {"error": ...} when rocm-smi is unavailable."""
+    """Current and maximum shader clock, memory clock, junction temperature and
+    package power of GPU 0 ({"error": ...} when rocm-smi is unavailable)."""
     try:
-        out = subprocess.run(["rocm-smi", "--showclocks", "--showtemp", "--json"],
-                             capture_output=True, text=True, timeout=30).stdout
-        card = next(iter(json.loads(out).values()))
+        card = _smi_json("--showclocks", "--showtemp", "--showpower")
     except Exception as e:  # the report still stands without it
         return {"error": str(e)[:200]}
 
-    def mhz(key_part):
+    def find(pred, conv):
         for key, value in card.items():
-            if key_part in key.lower():
-                m = re.search(r"(\d+)\s*mhz", str(value).lower())
-                if m:
-                    return int(m.group(1))
+            if pred(key.lower()):
+                try:
+                    return conv(str(value))
+                except ValueError:
+                    pass
         return -1
 
-    temp = -1
-    for key, value in card.items():
-        if "temperature" in key.lower() and "edge" in key.lower():
-            try:
-                temp = int(float(value))
-            except ValueError:
-                pass
-    state = {"sclk_mhz": mhz("sclk"), "mclk_mhz": mhz("mclk"), "temperature_c": temp}
-    state["sclk_max_mhz"] = _max_sclk()
-    return state
+    def mhz(text):
+        m = re.search(r"(\d+)\s*mhz", text.lower())
+        if not m:
+            raise ValueError(text)
+        return int(m.group(1))
+
+    return {"sclk_mhz": find(lambda k: k.startswith("sclk clock speed"), mhz),
+            "mclk_mhz": find(lambda k: k.startswith("mclk clock speed"), mhz),
+            "temperature_c": find(lambda k: "temperature" in k and "junction" in k,
+                                  lambda v: int(float(v))),
+            "power_w": find(lambda k: "power" in k and "max" not in k,
+                            lambda v: float(v)),
+            "sclk_max_mhz": _max_sclk()}
 
 
 _MAX_SCLK = None
 
 
 def _max_sclk() -> int:
+    """Highest shader clock level rocm-smi lists (-1 if unknown)."""
     global _MAX_SCLK
     if _MAX_SCLK is None:
         _MAX_SCLK = -1
         try:
-            out = subprocess.run(["rocm-smi", "--showsclkrange", "--json"],
-                                 capture_output=True, text=True, timeout=30).stdout
-            nums = [int(x) for x in re.findall(r"(\d+)\s*[Mm][Hh]z", out)]
+            out = subprocess.run(["rocm-smi", "--showclkfrq"], capture_output=True,
+                                 text=True, timeout=30).stdout
+            sect = out.split("sclk", 1)[1] if "sclk" in out else ""
+            sect = re.split(r"Supported \w+ frequencies|mclk|fclk|socclk", sect)[0]
+            nums = [int(x) for x in re.findall(r"(\d+)\s*[Mm][Hh]z", sect)]
             _MAX_SCLK = max(nums) if nums else -1
         except Exception:
             pass
