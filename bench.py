@@ -57,14 +57,15 @@ def time_workload(w, steps: int, warmup: int, device):
             bias = bias.float()
     tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
     tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
+    launch = desc.bind(A, B, C, ws, stream=stream, bias=bias)
     for _ in range(warmup):
-        desc.launch(A, B, C, ws, stream=stream, bias=bias)
+        launch()
     region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     torch.cuda.synchronize(device)
     t0 = time.perf_counter()
     region[0].record(stream)
     for i in range(steps):
-        desc.launch(A, B, C, ws, stream=stream, bias=bias)
+        launch()
     region[1].record(stream)
     torch.cuda.synchronize(device)
     wall = time.perf_counter() - t0
@@ -182,7 +183,7 @@ def main() -> int:
             if other.name == w.name:
                 continue
             steps = 200 if other.flop < 1e9 else (50 if other.flop < 2e11 else 10)
-            o = time_workload(other, steps, 5, device)
+            o = time_workload(other, steps, steps, device)
             us = o["avg_launch_ms"] * 1e3
             wall_us = o["wall_s"] * 1e6 / steps
             extra[other.name] = {

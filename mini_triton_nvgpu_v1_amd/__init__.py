@@ -198,6 +198,26 @@ class GemmDesc:
                                            _ptr(bias), _ptr(workspace),
                                            _stream_handle(stream)))
 
+    def bind(self, a, b, c, workspace=None, stream=None, bias=None):
+        """A zero-argument launcher for repeated launches on the same buffers
+        and stream: device addresses and the stream handle are resolved once,
+        so each call is one C call (the shape of the reference's driver loop,
+        tools/bench_stage1_fair.py:680-699). The buffers must outlive it."""
+        L = lib()
+        args = (self._h, _ptr(a), _ptr(b), _ptr(c))
+        ws, st = _ptr(workspace), _stream_handle(stream)
+        if bias is None:
+            fn, args = L.tb_gemm_launch, args + (ws, st)
+        else:
+            fn, args = L.tb_gemm_launch_ex, args + (_ptr(bias), ws, st)
+        keep = (self, a, b, c, workspace, bias)  # hold the buffers and descriptor
+
+        def launch() -> None:
+            if fn(*args):
+                _check(-1)
+        launch.keep = keep
+        return launch
+
     def close(self) -> None:
         if self._h and self._h.value:
             lib().tb_desc_free(self._h)

@@ -75,15 +75,24 @@ struct EpiArgs {
   float lo, hi;
 };
 
+// x / (1 + e^-z) with the hardware exp2 (v_exp_f32) and reciprocal
+// (v_rcp_f32), each about 1 ulp: e^-z = 2^(-z log2 e). For z -> -inf the
+// denominator is +inf and the result 0; for z -> +inf it is x.
+__device__ __forceinline__ float epi_x_sigmoid(float x, float z) {
+  const float e = __builtin_amdgcn_exp2f(-z * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.f + e);
+}
+
 __device__ __forceinline__ float epi_activation(float x, int act) {
   if (act == 1)
     return x > 0.f ? x : 0.f;
-  if (act == 2) { // tanh form of GELU (Hendrycks & Gimpel, 2016)
-    const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.f + tanhf(u));
+  if (act == 2) { // tanh form of GELU (Hendrycks & Gimpel, 2016):
+    // 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
+    const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
+    return epi_x_sigmoid(x, u2);
   }
-  if (act == 3)
-    return x / (1.f + expf(-x));
+  if (act == 3) // SiLU: x sigmoid(x)
+    return epi_x_sigmoid(x, x);
   return x;
 }
 

@@ -530,26 +530,29 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     const int ccol_base = n0 + wn * T::WTN + 4 * khalf;
 
     // Fused epilogue steps (bias, activation, clamp) on the whole f32 result,
-    // in place on the accumulators, one 32-column tile j at a time so a lane
-    // holds only that tile's 16 bias values. C += A*B applies them in its
-    // store loop, after the prior C is added. EPI instances are never
-    // launched for split-K partials (the reduction applies the steps there)
-    // nor with atomic output.
+    // in place on the accumulators, one 32-column tile j at a time. C += A*B
+    // applies them in its store loop, after the prior C is added. EPI
+    // instances are never launched for split-K partials (the reduction
+    // applies the steps there) nor with atomic output.
     const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
     if constexpr (EPI && (OUT == kOutF16 || OUT == kOutF32Partial)) {
+      // every bias load of the wave tile first: one memory latency, not one
+      // per 32-column tile
+      epi_f32x4 bv[TN][4];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        epi_f32x4 bv[4];
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          bv[g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
+          bv[j][g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int g = 0; g < 4; ++g)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              acc[i][j][4 * g + r] = epi_apply1(acc[i][j][4 * g + r], bv[g][r], ea);
+              acc[i][j][4 * g + r] = epi_apply1(acc[i][j][4 * g + r], bv[j][g][r], ea);
         __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
       }
     }

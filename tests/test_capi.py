@@ -128,3 +128,16 @@ def test_fused_epilogue_instances_and_bias_arguments():
         biased.launch(16, 16, 16, bias=260)
     with pytest.raises(tb.TbError, match="device pointers"):
         biased.launch(0, 0, 0, bias=256)
+
+
+def test_bound_launcher_checks_like_launch():
+    """GemmDesc.bind resolves the arguments once; its calls report the same
+    argument errors as launch (checked before any GPU call)."""
+    biased = tb.GemmDesc.from_config(_cfg(epi_bias=tb.EPI_BIAS_F32))
+    with pytest.raises(tb.TbError, match="tb_gemm_launch_ex"):
+        biased.bind(16, 16, 16)()
+    with pytest.raises(tb.TbError, match="16-byte aligned"):
+        biased.bind(16, 16, 16, bias=260)()
+    plain = tb.GemmDesc.from_config(_cfg())
+    with pytest.raises(tb.TbError, match="device pointers"):
+        plain.bind(0, 16, 16)()

@@ -6,10 +6,11 @@ pipeline and the C ABI (tb_gemm_launch_ex with the bias vector), except the
 plain-f32-store case, which only a direct descriptor reaches. The oracle
 computes [C0 +] A@B in f64, then tbo_epilogue_f64 (bias, activation, clamp),
 and every element must satisfy |got - ref| <= 1e-2 * (|ref| + 1). The
-kernels compute the steps in f32 (tanhf / expf of the device math library),
-well inside that bound. The reference declares these expr kinds but has no
-implementation to compare with; the oracle's formulas are pinned to torch's
-CPU GELU/SiLU and to closed forms in tests/test_oracle.py.
+kernels compute the steps in f32 (GELU and SiLU as x * sigmoid(z) from the
+hardware exp2 and reciprocal, about 1 ulp each), well inside that bound. The
+reference declares these expr kinds but has no implementation to compare
+with; the oracle's formulas are pinned to torch's CPU GELU/SiLU and to closed
+forms in tests/test_oracle.py.
 """
 import dataclasses
 
