@@ -50,8 +50,14 @@ def main() -> int:
           if desc.workspace_bytes else None)
     tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
     tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
+    bias = None
+    if w.bias:  # fused bias step: N seeded values
+        bias = torch.empty((1, w.N), dtype=torch.float16, device=dev)
+        tb.fill_seeded_f16(bias, 1, w.N, w.seed ^ 0xB1A5, 0, 1.0, stream=stream)
+        if w.bias == "f32":
+            bias = bias.float()
     for _ in range(args.reps):
-        desc.launch(A, B, C, ws, stream=stream)
+        desc.launch(A, B, C, ws, stream=stream, bias=bias)
     torch.cuda.synchronize()
     print(f"profiling: {args.reps} launches of {desc.kernel_name} ({w.name})", flush=True)
     if args.hipblaslt:
