@@ -387,7 +387,8 @@ def preheat_gpu(runner: CaseRunner, warmup: int, iters: int, max_attempts: int,
 def rocprof_case(case: FairCase, out_dir: Path, args) -> dict[str, Any]:
     """rocprofv3 --kernel-trace --stats over one round of this case, in a child
     process (the profiler must start its own program)."""
-    cdir = out_dir / case.name / "rocprof"
+    # absolute: the profiler runs from TMPDIR
+    cdir = (out_dir / case.name / "rocprof").resolve()
     cdir.mkdir(parents=True, exist_ok=True)
     cmd = ["rocprofv3", "--kernel-trace", "--stats", "--output-format", "csv",
            "-d", str(cdir), "-o", "trace", "--", sys.executable, "-m",
@@ -401,9 +402,10 @@ def rocprof_case(case: FairCase, out_dir: Path, args) -> dict[str, Any]:
                            cwd=os.environ.get("TMPDIR", "/tmp"))
     except Exception as e:
         return {"ok": False, "error": str(e)[:300]}
+    (cdir / "rocprof.log").write_text(p.stdout + p.stderr)
     stats = sorted(cdir.rglob("*kernel_stats.csv"))
     return {"ok": p.returncode in (0, 139) and bool(stats), "returncode": p.returncode,
-            "kernel_stats": [str(s) for s in stats]}
+            "kernel_stats": [str(s) for s in stats], "log": str(cdir / "rocprof.log")}
 
 
 def parse_args(argv=None) -> argparse.Namespace:
