@@ -171,21 +171,25 @@ RAGGED = Workload("ragged_96x80x32", 96, 80, 32, 0x5EED0002, UNIFORM,
                   (64, 64, 32), num_waves=4, exact_tile=False)
 RAGGED_128 = Workload("tile_128x128x32", 128, 128, 32, 0x5EED0003, UNIFORM,
                       (128, 128, 32), num_waves=4)
-# 8 waves = 2 per SIMD on the 256x256 tile: one wave's MFMAs run while the
-# other waits on LDS reads or the barrier (~5% over 4 waves)
+# 4 waves of 128x128 (one per SIMD) on the 256x256 tile: a third fewer LDS
+# fragment bytes per MFMA than 8 waves of 64x128, so less energy per launch
+# and a higher sustained clock; the exact-shape kernel of this instance keeps
+# its lone wave per SIMD busy (about 4% faster than 8 waves)
 ROOFLINE = Workload("gemm_4096", 4096, 4096, 4096, 0x5EED0004, NORMAL,
-                    (256, 256, 64), num_waves=8, stages=2, group_m=8)
+                    (256, 256, 64), num_waves=4, stages=2, group_m=8)
 # 128x64 tiles with 3 LDS stages: 32 tiles x 8 splits = 256 workgroups, one
 # per CU (128x128 tiles would leave half the CUs idle)
 SPLIT_K = Workload("splitk_512x512x16384", 512, 512, 16384, 0x5EED0005,
                    UNIFORM, (128, 64, 64), num_waves=4, stages=3, split_k=8)
 PERSISTENT = Workload("persistent_8192", 8192, 8192, 8192, 0x5EED0006, NORMAL,
-                      (256, 256, 64), num_waves=8, group_m=8, persistent=True,
+                      (256, 256, 64), num_waves=4, group_m=8, persistent=True,
                       num_ctas=256)
 
 ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]
 # The roofline GEMM with fused epilogue steps (a bias row and the tanh GELU
-# on the f32 result before the f16 store): what the fusion costs.
+# on the f32 result before the f16 store): what the fusion costs. 8 waves:
+# the GELU's VALU work at the end of a tile overlaps the sibling wave's
+# MFMAs, which a lone wave per SIMD cannot do (8 waves measure ~4% faster).
 FUSED = [dataclasses.replace(ROOFLINE, name="gemm_4096_bias_gelu", bias="f16",
-                             activation="gelu_tanh")]
+                             activation="gelu_tanh", num_waves=8)]
 BY_NAME = {w.name: w for w in ALL + FUSED}

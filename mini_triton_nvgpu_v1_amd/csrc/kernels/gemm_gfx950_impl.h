@@ -4,6 +4,9 @@
 
 #include "gemm_gfx950.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace tbk {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -50,6 +53,29 @@ __device__ __forceinline__ void load_lds16(u32x4 rsrc, uint32_t lds_base,
                :
                : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
                : "memory");
+}
+
+// The same with M0 = lds_base + OFF, OFF a constant: the sum is formed in
+// M0 itself, so a kernel with many load rounds and stages keeps one LDS base
+// in an SGPR instead of one per (stage, round).
+template <uint32_t OFF>
+__device__ __forceinline__ void load_lds16_at(u32x4 rsrc, uint32_t lds_base, uint32_t voff,
+                                              uint32_t soff) {
+  asm volatile("s_add_u32 m0, %0, %4\n\t"
+               "buffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff), "i"(OFF)
+               : "memory", "scc");
+}
+
+// f(std::integral_constant<int, i>{}) for i = 0 .. N-1, in order.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
 // Raw buffer descriptor as four dwords for inline asm operands.
@@ -210,6 +236,276 @@ __device__ __forceinline__ void sched_step() {
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     if (i < NVMEM)
       __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+  }
+}
+
+// ---- 4 waves of 128x128 on a 256x256x64 tile, exact shapes ----------------------
+// One wave per SIMD, 2 LDS stages, M and N multiples of 256, K of 64 (tile,
+// grouped or persistent order; f16 C). The LDS ring, its swizzles, the
+// fragments and the MFMA k order are those of the general loop, so C is
+// bit-identical to it; the instruction stream is what changes. A lone wave
+// per SIMD has no sibling to run its MFMAs while it computes addresses or
+// waits, so:
+//  * every address is fixed before the loop: one vector offset per operand,
+//    scalar offsets per load round, and per-stage LDS bases; the k step, row
+//    group and B half-fragment ride in the ds_read immediate offset;
+//  * no per-load bounds checks: tiles are whole, and the ring's lookahead
+//    loads past the last k-tile use a descriptor of zero records (zeros);
+//  * one loop iteration runs from a k-tile's barrier to the next, so the
+//    fragment reads in flight at the back-edge are consumed already and no
+//    lgkmcnt(0) lands in front of the first MFMAs of a k-tile;
+//  * the barrier is vmcnt(0) + s_barrier: every LDS read before it has been
+//    consumed by an MFMA (hence waited for), and the stage it frees is only
+//    written by the refill loads issued after it.
+// Slot schedule per 16-deep k step: MFMA m (A row group m/4, B column group
+// m%4), and, in slot (4o)/3, read o of the next k step in the order A0, B0
+// (two halves), B1, B2, B3, A1, A2, A3. The barrier sits after MFMA 7 of the
+// last k step; the first reads of the next k-tile and its refill follow it.
+template <bool EPI>
+__device__ __forceinline__ void wide4_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
+  constexpr int BK = 64;
+  constexpr uint32_t SLOT = 65536; // ring slot: A [256][64] at 0, B [64][256] at 32 KiB
+  constexpr uint32_t B_AT = 32768;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1, khalf = lane >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(TBK_LDS void *)lds;
+  const int nk = p.K / BK;
+
+  // Direct loads: round l of wave w fills 1 KiB at slot + l * 4 KiB + w * 1 KiB
+  // (A rows 32l + 8w .. +7; B k-rows 8l + 2w, +1). The swizzle phase repeats
+  // every 16 A rows and every 4 B rows, so a lane fetches the same logical
+  // chunk in every round and only the scalar offset moves.
+  const int a_row0 = (wave * 64 + lane) >> 3;
+  const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
+  const uint32_t a_voff = ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + a_lc * 8) * 2u;
+  const int b_row0 = (wave * 64 + lane) >> 5;
+  const int b_lc = (lane & 31) ^ (4 * (b_row0 & 3));
+  const uint32_t b_voff =
+      ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + b_lc * 8)) * 2u;
+  const uint32_t a_round = 32u * (uint32_t)p.lda * 2u, b_round = 8u * (uint32_t)p.ldb * 2u;
+  const uint32_t a_ktile = BK * 2u, b_ktile = BK * 2u * (uint32_t)p.ldb;
+  const uint32_t a_bytes = (uint32_t)p.M * (uint32_t)p.lda * 2u;
+  const uint32_t b_bytes = (uint32_t)p.K * (uint32_t)p.ldb * 2u;
+  const uint32_t wlds = lds0 + wave * 1024u;
+  // load l of k-tile kt into ring slot ST (l is a constant once unrolled:
+  // the LDS offset becomes the literal of the M0 add)
+  auto load = [&](const u32x4 &ra, const u32x4 &rb, int kt, auto st_c, int l) {
+    constexpr uint32_t base = decltype(st_c)::value * SLOT;
+    static_for<16>([&](auto l_c) {
+      constexpr int L = decltype(l_c)::value;
+      if (L == l) {
+        if constexpr (L < 8)
+          load_lds16_at<base + L * 4096u>(ra, wlds, a_voff,
+                                          (uint32_t)kt * a_ktile + L * a_round);
+        else
+          load_lds16_at<base + B_AT + (L - 8) * 4096u>(rb, wlds, b_voff,
+                                                       (uint32_t)kt * b_ktile +
+                                                           (L - 8) * b_round);
+      }
+    });
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1c = std::integral_constant<int, 1>;
+
+  // Fragment reads: A fragment i of k step ks from stage st is one
+  // ds_read_b128 at a_base[st][ks] + i * 4 KiB; half r of B fragment j is a
+  // ds_read_b64_tr_b16 at b_base[st][j] + ks * 8 KiB + r * 2 KiB.
+  const int a_ph = ((lane & 31) >> 1) & 7; // (row / 2) % 8 of every row the lane reads
+  const int tr_k = 8 * khalf + ((lane & 15) >> 2);
+  const int b_ph = (lane >> 2) & 3;        // k % 4 of every k row the lane reads
+  uint32_t a_base[2][4], b_base[2][4];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      a_base[st][q] = lds0 + st * SLOT + (wm * 128 + (lane & 31)) * 128 +
+                      (((2 * q + khalf) ^ a_ph) * 16);
+      b_base[st][q] = lds0 + st * SLOT + B_AT + tr_k * 512 + wn * 256 +
+                      32 * ((lane >> 4) & 1) + 16 * ((lane & 3) >> 1) + 8 * (lane & 1) +
+                      64 * (q ^ b_ph);
+    }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = (f32x16){};
+  half8 fa[2][4], fb[2][4];
+  auto rd = [&](int buf, int st, int ks, int o) {
+    if (o == 0 || o >= 9) {
+      const int i = o == 0 ? 0 : o - 8;
+      fa[buf][i] = __builtin_bit_cast(
+          half8, *(const TBK_LDS u32x4 *)(uintptr_t)(a_base[st][ks] + i * 4096));
+    } else {
+      const int j = (o - 1) >> 1, r = (o - 1) & 1;
+      const half4 h = __builtin_bit_cast(
+          half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TBK_LDS short4 *)(uintptr_t)(
+                     b_base[st][j] + ks * 8192 + r * 2048)));
+      if (r == 0)
+        fb[buf][j].lo = h;
+      else
+        fb[buf][j].hi = h;
+    }
+  };
+  auto mfma = [&](int buf, int m) {
+    const int i = m >> 2, j = m & 3;
+    acc[i][j] =
+        __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+  };
+  auto barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // MFMAs m_lo .. m_hi-1 of k step ks (stage st), the reads of k step ks+1
+  // and whatever `extra` issues in slot m
+  auto kstep = [&](int st, int ks, int m_lo, int m_hi, auto &&extra) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      if (m < m_lo || m >= m_hi)
+        continue;
+      mfma(ks & 1, m);
+      if (ks < 3) {
+#pragma unroll
+        for (int o = 0; o < 12; ++o)
+          if ((4 * o) / 3 == m)
+            rd((ks + 1) & 1, st, ks + 1, o);
+      }
+      extra(m);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto nothing = [](int) {};
+
+  // prologue: k-tiles 0 and 1 in flight, wait for 0, run it up to its barrier
+  {
+    const u32x4 ra = rsrc_dwords(p.A, a_bytes), rb = rsrc_dwords(p.B, b_bytes);
+    const u32x4 ra1 = rsrc_dwords(p.A, nk > 1 ? a_bytes : 0u);
+    const u32x4 rb1 = rsrc_dwords(p.B, nk > 1 ? b_bytes : 0u);
+#pragma unroll
+    for (int l = 0; l < 16; ++l)
+      load(ra, rb, 0, S0{}, l);
+#pragma unroll
+    for (int l = 0; l < 16; ++l)
+      load(ra1, rb1, 1, S1c{}, l);
+  }
+  wait_vmcnt<16>();
+  barrier();
+#pragma unroll
+  for (int o = 0; o < 12; ++o)
+    rd(0, 0, 0, o);
+  kstep(0, 0, 0, 16, nothing);
+  kstep(0, 1, 0, 16, nothing);
+  kstep(0, 2, 0, 16, nothing);
+  kstep(0, 3, 0, 8, nothing);
+
+  // body(it): k-tile it (stage S) from its barrier on, k-tile it+1 (stage
+  // S^1) up to its barrier; stage S is refilled with k-tile it+2, loads 0..7
+  // after the barrier and 8..15 in the first slots of k-tile it+1.
+  auto body = [&](int it, auto stage) {
+    constexpr int S = decltype(stage)::value, S1 = S ^ 1;
+    const bool ok = it + 2 < nk;
+    const u32x4 ra = rsrc_dwords(p.A, ok ? a_bytes : 0u);
+    const u32x4 rb = rsrc_dwords(p.B, ok ? b_bytes : 0u);
+    wait_vmcnt<0>(); // k-tile it+1 landed (this wave's part)
+    barrier();
+#pragma unroll
+    for (int m = 8; m < 16; ++m) {
+      mfma(1, m);
+#pragma unroll
+      for (int o = 0; o < 12; ++o)
+        if (8 + (2 * o) / 3 == m)
+          rd(0, S1, 0, o);
+      load(ra, rb, it + 2, stage, m - 8);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    auto refill = [&](int m) {
+      if (m < 8)
+        load(ra, rb, it + 2, stage, 8 + m);
+    };
+    kstep(S1, 0, 0, 16, refill);
+    kstep(S1, 1, 0, 16, nothing);
+    kstep(S1, 2, 0, 16, nothing);
+    kstep(S1, 3, 0, 8, nothing);
+  };
+  int it = 0;
+  for (; it + 2 <= nk - 1; it += 2) {
+    body(it, S0{});
+    body(it + 1, S1c{});
+  }
+  if (it < nk - 1)
+    body(it, S0{});
+#pragma unroll
+  for (int m = 8; m < 16; ++m) { // the last k-tile after its barrier point
+    mfma(1, m);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmcnt<0>(); // the zero loads past the end have landed too
+
+  // f16 C through LDS (as the staged epilogue of the general loop): each
+  // wave's 128x128 tile goes to its own 32 KiB, 256-byte rows, chunk c of row
+  // r at c ^ (r % 16) with the 8-byte halves swapped on odd 16-row groups,
+  // and comes back as 4 whole rows per ds_read_b128 / buffer store. The
+  // fused steps (bias, activation, clamp) run on each 32x32 tile's f32
+  // values on their way to LDS, so only one tile is out of the accumulators
+  // at a time.
+  // The epilogue's lane-derived addresses are computed from an opaque copy
+  // of the lane index, so the compiler cannot hoist them out of a persistent
+  // tile loop and keep them live (in registers the main loop needs).
+  int el = lane;
+  asm volatile("" : "+v"(el));
+  const int ehalf = el >> 5;
+  const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
+  epi_f32x4 bv[EPI ? 4 : 1][EPI ? 4 : 1];
+  if constexpr (EPI) { // every bias load first: one memory latency
+    const int ccol = n0 + wn * 128 + 4 * ehalf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        bv[j][g] = epi_load_bias(ea, ccol + j * 32 + 8 * g, p.N);
+  }
+  barrier(); // every wave is past its last fragment read and load
+  TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 32 + (el & 31);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = acc[i][j][4 * g + e];
+          if constexpr (EPI)
+            x[e] = epi_apply1(x[e], bv[j][g][e], ea);
+        }
+        u32x2 v;
+        v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
+        v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
+        const int chunk = (4 * j + g) ^ (r & 15);
+        const int half = ehalf ^ ((r >> 4) & 1);
+        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
+  const int q = el & 15;
+#pragma unroll
+  for (int t = 0; t < 32; ++t) {
+    const int r = t * 4 + (el >> 4);
+    u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
+    if ((r >> 4) & 1)
+      v = (u32x4){v[2], v[3], v[0], v[1]};
+    const uint32_t off = ((uint32_t)(m0 + wm * 128 + r) * (uint32_t)p.ldc +
+                          (uint32_t)(n0 + wn * 128 + 8 * q)) * 2u;
+    __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
   }
 }
 
@@ -790,6 +1086,39 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   }
 }
 
+// The exact-shape kernel of the 4-wave 256x256x64 2-stage f16 instance: the
+// launcher runs it instead of gemm_kernel when M, N, K are whole tiles and
+// the order is tile, grouped or persistent (GemmParams::exact). A kernel of
+// its own, so that its register allocation is not the general loop's.
+template <bool EPI>
+__global__ __launch_bounds__(256, 1) void gemm_wide4(GemmParams p) {
+  __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
+  const bool persistent =
+      p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
+  int prog = blockIdx.x;
+  const int nprog = gridDim.x;
+  if (p.xcds > 1 && (nprog % p.xcds) == 0)
+    prog = (prog % p.xcds) * (nprog / p.xcds) + prog / p.xcds;
+  for (int work = prog; work < p.total_work;
+       work += (persistent ? nprog : p.total_work)) {
+    int tile_m, tile_n, part;
+    map_program(p, work, tile_m, tile_n, part);
+    if (work != prog)
+      __syncthreads(); // every wave read its staged epilogue back
+    wide4_tile<EPI>(p, tile_m * 256, tile_n * 256, lds);
+  }
+}
+
+// The exact-shape kernel of an instance, or nullptr.
+template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int ST, bool EPI>
+inline const void *exact_kernel() {
+  if constexpr (BM == 256 && BN == 256 && BK == 64 && WGM == 2 && WGN == 2 && ST == 2 &&
+                OUT == kOutF16)
+    return reinterpret_cast<const void *>(&gemm_wide4<EPI>);
+  else
+    return nullptr;
+}
+
 } // namespace tbk
 
 // One registry entry per instance.
@@ -797,7 +1126,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   {{BM, BN, BK, WGM, WGN, OUT, ST, 0},                                           \
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST>),                        \
-   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT}
+   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT, \
+   tbk::exact_kernel<BM, BN, BK, WGM, WGN, OUT, ST, false>()}
 
 #define TBK_OUTS(BM, BN, BK, WGM, WGN, ST)                                      \
   TBK_ENTRY(BM, BN, BK, WGM, WGN, 0, ST), TBK_ENTRY(BM, BN, BK, WGM, WGN, 1, ST), \
@@ -811,7 +1141,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST, -1, true>),              \
    "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT \
-   "_epi"}
+   "_epi",                                                                       \
+   tbk::exact_kernel<BM, BN, BK, WGM, WGN, OUT, ST, true>()}
 
 #define TBK_EPI_OUTS(BM, BN, BK, WGM, WGN, ST)                                  \
   TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 0, ST),                                   \

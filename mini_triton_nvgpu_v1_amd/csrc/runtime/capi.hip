@@ -259,6 +259,8 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
   p.total_work = (int)d->total_work;
   p.xcds = cf.xcd_remap;
   p.ws_ld = (int)cf.n;
+  p.exact = cf.m % cf.block_m == 0 && cf.n % cf.block_n == 0 && cf.k % cf.block_k == 0 &&
+            cf.k > 0 && cf.mapping != TB_MAP_SPLIT_K;
   p.bias = bias;
   p.epi_bias = cf.epi_bias;
   p.epi_act = cf.epi_activation;
@@ -272,7 +274,8 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   void *args[] = {&p};
   const dim3 grid((unsigned)cf.num_programs), block((unsigned)(cf.num_waves * 64));
-  if (int rc = check_hip(hipLaunchKernel(d->entry->fn, grid, block, args, 0, s),
+  const void *fn = p.exact && d->entry->fn_exact ? d->entry->fn_exact : d->entry->fn;
+  if (int rc = check_hip(hipLaunchKernel(fn, grid, block, args, 0, s),
                          "hipLaunchKernel(gemm)"))
     return rc;
   if (cf.mapping == TB_MAP_SPLIT_K && cf.reduction == TB_RED_WORKSPACE) {

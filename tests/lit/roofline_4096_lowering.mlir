@@ -1,9 +1,9 @@
 // RUN: %tb-opt %s --pass-pipeline='builtin.module(tb-stage1-full-to-gfx950-pipeline{cubin-chip=gfx950})' | FileCheck %s
 
 // The roofline configuration: 4096^3 f16 -> f16, 256x256x64 tiles,
-// GROUP_M = 8, 8 waves (a 4x2 wave grid of 64x128 wave tiles): 256 programs
-// in two launch groups of 128, one per CU, in XCD-aware program order.
-module attributes {"tb.num-warps" = 8 : i64, "tb.requested-stages" = 2 : i64} {
+// GROUP_M = 8, 4 waves (a 2x2 wave grid of 128x128 wave tiles): 256 programs,
+// one per CU, in XCD-aware program order.
+module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {
   func.func @kernel(%A: memref<4096x4096xf16>, %B: memref<4096x4096xf16>,
                     %C: memref<4096x4096xf16>) {
     tb.matmul %A, %B, %C {block_m = 256 : i64, block_n = 256 : i64,
@@ -21,10 +21,10 @@ module attributes {"tb.num-warps" = 8 : i64, "tb.requested-stages" = 2 : i64} {
 // CHECK-SAME: num_sms = 256
 // CHECK-SAME: threads_per_warp = 64
 // CHECK: tb.gfx950_launch
-// CHECK-SAME: block = array<i64: 512, 1, 1>
+// CHECK-SAME: block = array<i64: 256, 1, 1>
 // CHECK-SAME: group_m = 8 : i64
 // CHECK-SAME: mapping = 1 : i64
 // CHECK-SAME: num_programs = 256 : i64
 // CHECK-SAME: xcd_remap = 8 : i64
-// CHECK-SAME: kernel = "tb_gemm_gfx950_256x256x64_w4x2_s2_out0"
+// CHECK-SAME: kernel = "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
 // CHECK-SAME: lds_bytes = 131072 : i64

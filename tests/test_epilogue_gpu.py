@@ -69,7 +69,8 @@ def _w(base, name, **kw):
 
 # f16 C through the plan pipeline: every epilogue store path of the kernel
 # (direct 8-byte stores, the LDS-staged stores of 64- and 128-wide wave
-# tiles, the split-K reduction, the persistent loop).
+# tiles, the exact-shape 4-wave 256x256 kernel, the split-K reduction, the
+# persistent loop).
 F16_CASES = [
     _w(configs.SMOKE, "smoke_bias16_relu", bias="f16", activation="relu"),
     _w(configs.RAGGED, "ragged_bias32_gelu_clamp", bias="f32", activation="gelu_tanh",
@@ -77,7 +78,9 @@ F16_CASES = [
     _w(configs.RAGGED_128, "tile128_bias16_silu_max", bias="f16", activation="silu",
        clamp_max=0.75),
     _w(configs.ROOFLINE, "w4x2_512_bias32_gelu", M=512, N=512, K=256, bias="f32",
-       activation="gelu_tanh"),
+       activation="gelu_tanh", num_waves=8),
+    _w(configs.ROOFLINE, "w2x2_512_bias16_silu", M=512, N=768, K=192, bias="f16",
+       activation="silu", clamp_min=-0.5),
     _w(configs.RAGGED, "ragged_clamp_only", clamp_min=-0.25),
     _w(configs.SPLIT_K, "splitk_bias16_silu", M=128, N=128, K=2048, bias="f16",
        activation="silu"),
