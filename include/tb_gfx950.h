@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TB_GFX950_ABI_VERSION 2
+#define TB_GFX950_ABI_VERSION 3
 
 /* element types (reference ScalarKind, include/tb/Analysis/KernelConfig.h:13-16) */
 #define TB_DTYPE_F16 0
@@ -62,6 +62,13 @@ extern "C" {
 #define TB_RED_NONE 0
 #define TB_RED_WORKSPACE 1
 #define TB_RED_ATOMIC 2
+
+/* MFMA instruction of the instance (reference MmaKind,
+ * include/tb/Analysis/KernelConfig.h:18-20, which names the mma.sync shape).
+ * 16x16x32 exists for the 4-wave 256x256x64 2-stage f16 tile on whole tiles
+ * (tile, grouped or persistent order): the plan selects it there. */
+#define TB_MFMA_32X32X16 0 /* v_mfma_f32_32x32x16_f16 */
+#define TB_MFMA_16X16X32 1 /* v_mfma_f32_16x16x32_f16 */
 
 /* fused epilogue steps (reference EpilogueExprKind LoadBias + Add,
  * Activation, Clamp; include/tb/Analysis/EpiloguePlan.h:61-75). They apply
@@ -101,6 +108,7 @@ typedef struct tb_gemm_config {
   int32_t epi_activation; /* TB_ACT_* */
   int32_t epi_clamp;     /* TB_CLAMP_* bits */
   float clamp_min, clamp_max; /* finite, clamp_min <= clamp_max when both */
+  int32_t mfma;          /* TB_MFMA_* (EncodingPlan instrShape) */
 } tb_gemm_config;
 
 typedef struct tb_gemm_desc tb_gemm_desc;

@@ -23,7 +23,8 @@ __all__ = [
     "MAP_GROUPED_TILE", "MAP_SPLIT_K", "MAP_PERSISTENT_TILE",
     "MAP_PERSISTENT_GROUPED", "RED_NONE", "RED_WORKSPACE", "RED_ATOMIC",
     "EPI_BIAS_NONE", "EPI_BIAS_F16", "EPI_BIAS_F32", "ACT_NONE", "ACT_RELU",
-    "ACT_GELU_TANH", "ACT_SILU", "CLAMP_MIN", "CLAMP_MAX",
+    "ACT_GELU_TANH", "ACT_SILU", "CLAMP_MIN", "CLAMP_MAX", "MFMA_32X32X16",
+    "MFMA_16X16X32",
 ]
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -39,6 +40,8 @@ RED_NONE, RED_WORKSPACE, RED_ATOMIC = 0, 1, 2
 EPI_BIAS_NONE, EPI_BIAS_F16, EPI_BIAS_F32 = 0, 1, 2
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 CLAMP_MIN, CLAMP_MAX = 1, 2
+# MFMA instruction of the instance (the EncodingPlan's instrShape)
+MFMA_32X32X16, MFMA_16X16X32 = 0, 1
 
 
 class TbError(RuntimeError):
@@ -60,7 +63,7 @@ class GemmConfig(ctypes.Structure):
         ("xcd_remap", ctypes.c_int32),
         ("epi_bias", ctypes.c_int32), ("epi_activation", ctypes.c_int32),
         ("epi_clamp", ctypes.c_int32), ("clamp_min", ctypes.c_float),
-        ("clamp_max", ctypes.c_float),
+        ("clamp_max", ctypes.c_float), ("mfma", ctypes.c_int32),
     ]
 
     def as_dict(self) -> dict:

@@ -17,7 +17,8 @@ from dataclasses import dataclass, field
 from . import (ACC_INIT_ZERO, ACT_GELU_TANH, ACT_NONE, ACT_RELU, ACT_SILU,
                CLAMP_MAX, CLAMP_MIN, DTYPE_F16, EPI_BIAS_F16, EPI_BIAS_F32,
                EPI_BIAS_NONE, MAP_GROUPED_TILE, MAP_PERSISTENT_GROUPED,
-               MAP_SPLIT_K, MAP_TILE, RED_NONE, RED_WORKSPACE, GemmConfig)
+               MAP_SPLIT_K, MAP_TILE, MFMA_16X16X32, MFMA_32X32X16, RED_NONE,
+               RED_WORKSPACE, GemmConfig)
 
 ACTIVATIONS = {"": ACT_NONE, "relu": ACT_RELU, "gelu_tanh": ACT_GELU_TANH,
                "silu": ACT_SILU}
@@ -162,7 +163,15 @@ class Workload:
             epi_activation=ACTIVATIONS[self.activation],
             epi_clamp=(CLAMP_MIN if self.clamp_min is not None else 0)
             | (CLAMP_MAX if self.clamp_max is not None else 0),
-            clamp_min=self.clamp_min or 0.0, clamp_max=self.clamp_max or 0.0)
+            clamp_min=self.clamp_min or 0.0, clamp_max=self.clamp_max or 0.0,
+            mfma=MFMA_16X16X32 if self.mfma16_supported() else MFMA_32X32X16)
+
+    def mfma16_supported(self) -> bool:
+        """The plan's choice of v_mfma_f32_16x16x32_f16: the 4-wave
+        256x256x64 2-stage f16 tile on whole tiles, no split-K."""
+        return (self.block == (256, 256, 64) and self.num_waves == 4 and self.stages == 2
+                and self.M % 256 == 0 and self.N % 256 == 0 and self.K % 64 == 0
+                and self.split_k == 1)
 
 
 SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,
@@ -172,9 +181,10 @@ RAGGED = Workload("ragged_96x80x32", 96, 80, 32, 0x5EED0002, UNIFORM,
 RAGGED_128 = Workload("tile_128x128x32", 128, 128, 32, 0x5EED0003, UNIFORM,
                       (128, 128, 32), num_waves=4)
 # 4 waves of 128x128 (one per SIMD) on the 256x256 tile: a third fewer LDS
-# fragment bytes per MFMA than 8 waves of 64x128, so less energy per launch
-# and a higher sustained clock; the exact-shape kernel of this instance keeps
-# its lone wave per SIMD busy (about 4% faster than 8 waves)
+# fragment bytes per MFMA than 8 waves of 64x128, and (whole tiles) the
+# 16x16x32 instance, a quarter of the accumulator register traffic per FLOP:
+# less energy per launch, a higher sustained clock on this power-limited part
+# (~14% faster than 8 waves of 32x32x16)
 ROOFLINE = Workload("gemm_4096", 4096, 4096, 4096, 0x5EED0004, NORMAL,
                     (256, 256, 64), num_waves=4, stages=2, group_m=8)
 # 128x64 tiles with 3 LDS stages: 32 tiles x 8 splits = 256 workgroups, one
@@ -187,9 +197,7 @@ PERSISTENT = Workload("persistent_8192", 8192, 8192, 8192, 0x5EED0006, NORMAL,
 
 ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]
 # The roofline GEMM with fused epilogue steps (a bias row and the tanh GELU
-# on the f32 result before the f16 store): what the fusion costs. 8 waves:
-# the GELU's VALU work at the end of a tile overlaps the sibling wave's
-# MFMAs, which a lone wave per SIMD cannot do (8 waves measure ~4% faster).
+# on the f32 result before the f16 store): what the fusion costs.
 FUSED = [dataclasses.replace(ROOFLINE, name="gemm_4096_bias_gelu", bias="f16",
-                             activation="gelu_tanh", num_waves=8)]
+                             activation="gelu_tanh")]
 BY_NAME = {w.name: w for w in ALL + FUSED}

@@ -185,7 +185,7 @@ const KernelEntry *find_kernel(const KernelKey &k) {
     const KernelEntry *e = kernel_at(i);
     if (e->key.bm == k.bm && e->key.bn == k.bn && e->key.bk == k.bk &&
         e->key.wgm == k.wgm && e->key.wgn == k.wgn && e->key.out == k.out &&
-        e->key.stages == k.stages && e->key.epi == k.epi)
+        e->key.stages == k.stages && e->key.epi == k.epi && e->key.mfma == k.mfma)
       return e;
   }
   return nullptr;

@@ -59,7 +59,6 @@ struct GemmParams {
   int total_work; // programs (non-persistent) or work items (persistent)
   int xcds;       // > 1: remap program ids so neighbours share an XCD
   int ws_ld;      // leading dimension of the f32 partial output (elements)
-  int exact;      // 1: M, N multiples of the block, K of block_k, no split-K
   // fused epilogue: bias (0 none, 1 f16, 2 f32; N values), activation
   // (0 none, 1 relu, 2 gelu_tanh, 3 silu), clamp bits (1 min, 2 max)
   const void *bias;
@@ -127,16 +126,14 @@ __device__ __forceinline__ float epi_apply1(float x, float bias, const EpiArgs &
 
 struct KernelKey {
   int bm, bn, bk, wgm, wgn, out, stages;
-  int epi; // 1: the fused epilogue steps are compiled in
+  int epi;  // 1: the fused epilogue steps are compiled in
+  int mfma; // 0: v_mfma_f32_32x32x16_f16, 1: v_mfma_f32_16x16x32_f16
 };
 
 struct KernelEntry {
   KernelKey key;
   const void *fn;
   const char *name;
-  // the same instance specialised for exact shapes (GemmParams::exact), or
-  // nullptr: launched instead of fn when the shape allows
-  const void *fn_exact;
 };
 
 // Registry of compiled instances (defined in the instance files).

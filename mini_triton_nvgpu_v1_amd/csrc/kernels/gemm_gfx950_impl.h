@@ -239,36 +239,57 @@ __device__ __forceinline__ void sched_step() {
   }
 }
 
-// ---- 4 waves of 128x128 on a 256x256x64 tile, exact shapes ----------------------
-// One wave per SIMD, 2 LDS stages, M and N multiples of 256, K of 64 (tile,
-// grouped or persistent order; f16 C). The LDS ring, its swizzles, the
-// fragments and the MFMA k order are those of the general loop, so C is
-// bit-identical to it; the instruction stream is what changes. A lone wave
-// per SIMD has no sibling to run its MFMAs while it computes addresses or
-// waits, so:
+// ---- 4 waves of 128x128 on a 256x256x64 tile with v_mfma_f32_16x16x32_f16 ------
+// The instance the plan selects for whole tiles of the 4-wave 256x256x64
+// 2-stage f16 configuration (mma = mfma_f32_16x16x32_f16): one wave per
+// SIMD, M and N multiples of 256, K of 64, tile / grouped / persistent order.
+// It fills the same LDS ring with the same swizzles as the general loop.
+//
+// Why 16x16x32: per FLOP it reads and writes a quarter of the accumulator
+// registers of 32x32x16 (4 f32 per 16x16x32 against 16 per 32x32x16 at half
+// the work), and this part is power-limited: same data movement, same MFMA
+// busy cycles, but a ~7% higher sustained clock and ~6% fewer cycles.
+//
+// The instruction stream is built for a lone wave per SIMD, which has no
+// sibling to run its MFMAs while it computes addresses or waits:
 //  * every address is fixed before the loop: one vector offset per operand,
-//    scalar offsets per load round, and per-stage LDS bases; the k step, row
-//    group and B half-fragment ride in the ds_read immediate offset;
+//    scalar offsets per load round, per-stage LDS bases; the k step, row
+//    group and B half ride in the ds_read immediate offset, and M0 is formed
+//    with an immediate add inside the load asm (no SGPR per stage and round);
 //  * no per-load bounds checks: tiles are whole, and the ring's lookahead
 //    loads past the last k-tile use a descriptor of zero records (zeros);
 //  * one loop iteration runs from a k-tile's barrier to the next, so the
 //    fragment reads in flight at the back-edge are consumed already and no
-//    lgkmcnt(0) lands in front of the first MFMAs of a k-tile;
-//  * the barrier is vmcnt(0) + s_barrier: every LDS read before it has been
-//    consumed by an MFMA (hence waited for), and the stage it frees is only
-//    written by the refill loads issued after it.
-// Slot schedule per 16-deep k step: MFMA m (A row group m/4, B column group
-// m%4), and, in slot (4o)/3, read o of the next k step in the order A0, B0
-// (two halves), B1, B2, B3, A1, A2, A3. The barrier sits after MFMA 7 of the
-// last k step; the first reads of the next k-tile and its refill follow it.
+//    lgkmcnt(0) lands in front of the first MFMAs of a k-tile; the barrier is
+//    vmcnt(0) + s_barrier (every LDS read before it has been consumed by an
+//    MFMA, and the stage it frees is only written by loads issued after it).
+// The MFMA is inline asm with the accumulator tied in place ("+a"): the
+// builtin's register allocation rotates 16x16 accumulators through copies
+// (dst != srcC), 248 extra moves per two k-tiles. Asm carries no hazard
+// information, so (a) each accumulator's first MFMA takes srcC = 0 (no
+// zeroing write right before it), (b) 24 wait states separate the last MFMA
+// from the first accumulator read, and (c) every fragment register is
+// rewritten at least 8 MFMA slots after its last MFMA read. LDS results are
+// waited for by the compiler's lgkmcnt tracking of the asm operands.
+//
+// Per 16x16x32 tile ii, jj (0..7) of the wave's 128x128: lane l holds
+// A[16ii + l%16][k0 + 8(l/16) .. +7] (one ds_read_b128) and
+// B[k0 + 8(l/16) .. +7][16jj + l%16] (two ds_read_b64_tr_b16); the product is
+// formed as C^T += B^T A^T, so lane l ends with C[16ii + l%16][16jj + 4(l/16)
+// + r], r = 0..3. Slot schedule per 32-deep k step (64 MFMAs, m = 8ii + jj):
+// the reads of the next k step in the order A0, B0 (two halves) .. B7, A1 ..
+// A7, op o in slot 8o/3; the barrier before slot 40 of the last k step; after
+// it the next k-tile's first reads (op o in slot 40 + o) and its refill
+// (loads 0..7 in the even slots 40..54, 8..15 in the odd slots 1..15 of the
+// next k-tile).
 template <bool EPI>
-__device__ __forceinline__ void wide4_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
-  constexpr int BK = 64;
+__device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
+  constexpr int BK = 64, BQ = 40;
   constexpr uint32_t SLOT = 65536; // ring slot: A [256][64] at 0, B [64][256] at 32 KiB
   constexpr uint32_t B_AT = 32768;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1, khalf = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(TBK_LDS void *)lds;
   const int nk = p.K / BK;
 
@@ -306,77 +327,92 @@ __device__ __forceinline__ void wide4_tile(const GemmParams &p, int m0, int n0, 
     });
   };
   using S0 = std::integral_constant<int, 0>;
-  using S1c = std::integral_constant<int, 1>;
+  using S1 = std::integral_constant<int, 1>;
 
-  // Fragment reads: A fragment i of k step ks from stage st is one
-  // ds_read_b128 at a_base[st][ks] + i * 4 KiB; half r of B fragment j is a
-  // ds_read_b64_tr_b16 at b_base[st][j] + ks * 8 KiB + r * 2 KiB.
-  const int a_ph = ((lane & 31) >> 1) & 7; // (row / 2) % 8 of every row the lane reads
-  const int tr_k = 8 * khalf + ((lane & 15) >> 2);
-  const int b_ph = (lane >> 2) & 3;        // k % 4 of every k row the lane reads
-  uint32_t a_base[2][4], b_base[2][4];
+  // Fragment reads. A tile ii of k step ks from stage st: one ds_read_b128 at
+  // a_base[st][ks] + ii * 2 KiB (16 rows of 128 bytes; the row phase
+  // (row / 2) % 8 = (l % 16) / 2 is the same for every ii). B tile jj: the 16
+  // lanes of group g = l / 16 read k rows 32ks + 8g + l%16/4 (+4 for the
+  // second half), columns 16jj + 4(l%4); with the B swizzle chunk ^ 4(k%4)
+  // the column group lands at 2(jj ^ 2(l%16/4)) 16-byte chunks.
+  const int g = lane >> 4, ta = (lane >> 2) & 3, tb = lane & 3;
+  uint32_t a_base[2][2], b_base[2][8];
 #pragma unroll
-  for (int st = 0; st < 2; ++st)
+  for (int st = 0; st < 2; ++st) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      a_base[st][q] = lds0 + st * SLOT + (wm * 128 + (lane & 31)) * 128 +
-                      (((2 * q + khalf) ^ a_ph) * 16);
-      b_base[st][q] = lds0 + st * SLOT + B_AT + tr_k * 512 + wn * 256 +
-                      32 * ((lane >> 4) & 1) + 16 * ((lane & 3) >> 1) + 8 * (lane & 1) +
-                      64 * (q ^ b_ph);
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      a_base[st][ks] = lds0 + st * SLOT + (wm * 128 + (lane & 15)) * 128 +
+                       (((4 * ks + g) ^ ((lane & 15) >> 1)) * 16);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      b_base[st][jj] = lds0 + st * SLOT + B_AT + (8 * g + ta) * 512 +
+                       (wn * 16 + 2 * (jj ^ (2 * ta)) + (tb >> 1)) * 16 + 8 * (tb & 1);
+  }
 
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc[i][j] = (f32x16){};
-  half8 fa[2][4], fb[2][4];
+  f32x4 acc[8][8];
+  half8 fa[2][8], fb[2][8];
+  // read op o (0..23) of k step ks into buffer buf: A0, B0 (halves 0, 1) ..
+  // B7, A1 .. A7
   auto rd = [&](int buf, int st, int ks, int o) {
-    if (o == 0 || o >= 9) {
-      const int i = o == 0 ? 0 : o - 8;
+    if (o == 0 || o >= 17) {
+      const int i = o == 0 ? 0 : o - 16;
       fa[buf][i] = __builtin_bit_cast(
-          half8, *(const TBK_LDS u32x4 *)(uintptr_t)(a_base[st][ks] + i * 4096));
+          half8, *(const TBK_LDS u32x4 *)(uintptr_t)(a_base[st][ks] + i * 2048));
     } else {
       const int j = (o - 1) >> 1, r = (o - 1) & 1;
       const half4 h = __builtin_bit_cast(
           half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TBK_LDS short4 *)(uintptr_t)(
-                     b_base[st][j] + ks * 8192 + r * 2048)));
+                     b_base[st][j] + ks * 16384 + r * 2048)));
       if (r == 0)
         fb[buf][j].lo = h;
       else
         fb[buf][j].hi = h;
     }
   };
-  auto mfma = [&](int buf, int m) {
-    const int i = m >> 2, j = m & 3;
-    acc[i][j] =
-        __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][j], fa[buf][i], acc[i][j], 0, 0, 0);
+  // MFMA m (tile m / 8, m % 8) of buffer buf; `first`: srcC = 0
+  auto mfma = [&](int buf, int m, bool first) {
+    const int i = m >> 3, j = m & 7;
+    if (first)
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0"
+                   : "=a"(acc[i][j])
+                   : "v"(fb[buf][j]), "v"(fa[buf][i]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                   : "+a"(acc[i][j])
+                   : "v"(fb[buf][j]), "v"(fa[buf][i]));
   };
   auto barrier = [&]() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // MFMAs m_lo .. m_hi-1 of k step ks (stage st), the reads of k step ks+1
-  // and whatever `extra` issues in slot m
-  auto kstep = [&](int st, int ks, int m_lo, int m_hi, auto &&extra) {
-#pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      if (m < m_lo || m >= m_hi)
-        continue;
-      mfma(ks & 1, m);
-      if (ks < 3) {
-#pragma unroll
-        for (int o = 0; o < 12; ++o)
-          if ((4 * o) / 3 == m)
-            rd((ks + 1) & 1, st, ks + 1, o);
-      }
+  // k step 0 (stage st): 64 MFMAs, the reads of k step 1, `extra` per slot
+  auto kstep0 = [&](int st, auto &&extra, bool first) {
+    static_for<64>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      mfma(0, m, first);
+      static_for<24>([&](auto o_c) {
+        constexpr int o = decltype(o_c)::value;
+        if constexpr ((8 * o) / 3 == m)
+          rd(1, st, 1, o);
+      });
       extra(m);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
   };
+  // k step 1, slots LO .. HI-1
+  auto kstep1 = [&](auto lo_c, auto hi_c) {
+    static_for<64>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      if constexpr (m >= decltype(lo_c)::value && m < decltype(hi_c)::value) {
+        mfma(1, m, false);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+  };
+  using Z = std::integral_constant<int, 0>;
+  using Q = std::integral_constant<int, BQ>;
+  using E = std::integral_constant<int, 64>;
   auto nothing = [](int) {};
 
   // prologue: k-tiles 0 and 1 in flight, wait for 0, run it up to its barrier
@@ -389,110 +425,93 @@ __device__ __forceinline__ void wide4_tile(const GemmParams &p, int m0, int n0, 
       load(ra, rb, 0, S0{}, l);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
-      load(ra1, rb1, 1, S1c{}, l);
+      load(ra1, rb1, 1, S1{}, l);
   }
   wait_vmcnt<16>();
   barrier();
 #pragma unroll
-  for (int o = 0; o < 12; ++o)
+  for (int o = 0; o < 24; ++o)
     rd(0, 0, 0, o);
-  kstep(0, 0, 0, 16, nothing);
-  kstep(0, 1, 0, 16, nothing);
-  kstep(0, 2, 0, 16, nothing);
-  kstep(0, 3, 0, 8, nothing);
+  kstep0(0, nothing, true);
+  kstep1(Z{}, Q{});
 
   // body(it): k-tile it (stage S) from its barrier on, k-tile it+1 (stage
-  // S^1) up to its barrier; stage S is refilled with k-tile it+2, loads 0..7
-  // after the barrier and 8..15 in the first slots of k-tile it+1.
+  // S^1) up to its barrier; stage S is refilled with k-tile it+2.
   auto body = [&](int it, auto stage) {
-    constexpr int S = decltype(stage)::value, S1 = S ^ 1;
+    constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(p.A, ok ? a_bytes : 0u);
     const u32x4 rb = rsrc_dwords(p.B, ok ? b_bytes : 0u);
     wait_vmcnt<0>(); // k-tile it+1 landed (this wave's part)
     barrier();
-#pragma unroll
-    for (int m = 8; m < 16; ++m) {
-      mfma(1, m);
-#pragma unroll
-      for (int o = 0; o < 12; ++o)
-        if (8 + (2 * o) / 3 == m)
-          rd(0, S1, 0, o);
-      load(ra, rb, it + 2, stage, m - 8);
+    static_for<64 - BQ>([&](auto s_c) {
+      constexpr int m = BQ + decltype(s_c)::value;
+      mfma(1, m, false);
+      rd(0, Sn, 0, m - BQ);
+      if constexpr (((m - BQ) & 1) == 0 && m - BQ < 16)
+        load(ra, rb, it + 2, stage, (m - BQ) >> 1);
       __builtin_amdgcn_sched_barrier(0);
-    }
+    });
     auto refill = [&](int m) {
-      if (m < 8)
-        load(ra, rb, it + 2, stage, 8 + m);
+      if ((m & 1) && m < 16)
+        load(ra, rb, it + 2, stage, 8 + (m >> 1));
     };
-    kstep(S1, 0, 0, 16, refill);
-    kstep(S1, 1, 0, 16, nothing);
-    kstep(S1, 2, 0, 16, nothing);
-    kstep(S1, 3, 0, 8, nothing);
+    kstep0(Sn, refill, false);
+    kstep1(Z{}, Q{});
   };
   int it = 0;
   for (; it + 2 <= nk - 1; it += 2) {
     body(it, S0{});
-    body(it + 1, S1c{});
+    body(it + 1, S1{});
   }
   if (it < nk - 1)
     body(it, S0{});
-#pragma unroll
-  for (int m = 8; m < 16; ++m) { // the last k-tile after its barrier point
-    mfma(1, m);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  kstep1(Q{}, E{}); // the last k-tile after its barrier point
+  // 24 wait states between the last MFMA and the first accumulator read
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   wait_vmcnt<0>(); // the zero loads past the end have landed too
 
-  // f16 C through LDS (as the staged epilogue of the general loop): each
-  // wave's 128x128 tile goes to its own 32 KiB, 256-byte rows, chunk c of row
-  // r at c ^ (r % 16) with the 8-byte halves swapped on odd 16-row groups,
-  // and comes back as 4 whole rows per ds_read_b128 / buffer store. The
-  // fused steps (bias, activation, clamp) run on each 32x32 tile's f32
-  // values on their way to LDS, so only one tile is out of the accumulators
-  // at a time.
-  // The epilogue's lane-derived addresses are computed from an opaque copy
-  // of the lane index, so the compiler cannot hoist them out of a persistent
-  // tile loop and keep them live (in registers the main loop needs).
+  // f16 C through LDS: each wave's 128x128 tile goes to its own 32 KiB,
+  // 256-byte rows, 16-byte chunk c of row r at c ^ (r % 16) (the 16 rows of a
+  // 16x16 tile then cover the 64 banks once), and comes back as 4 whole rows
+  // per ds_read_b128 / buffer store. The fused steps (bias, activation,
+  // clamp) run on each tile's f32 values on their way to LDS. The epilogue's
+  // lane-derived addresses come from an opaque copy of the lane index, so the
+  // compiler cannot hoist them out of a persistent tile loop and keep them
+  // live in registers the main loop needs.
   int el = lane;
   asm volatile("" : "+v"(el));
-  const int ehalf = el >> 5;
   const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
-  epi_f32x4 bv[EPI ? 4 : 1][EPI ? 4 : 1];
+  epi_f32x4 bv[EPI ? 8 : 1];
   if constexpr (EPI) { // every bias load first: one memory latency
-    const int ccol = n0 + wn * 128 + 4 * ehalf;
+    const int ccol = n0 + wn * 128 + 4 * (el >> 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        bv[j][g] = epi_load_bias(ea, ccol + j * 32 + 8 * g, p.N);
+    for (int j = 0; j < 8; ++j)
+      bv[j] = epi_load_bias(ea, ccol + 16 * j, p.N);
   }
   barrier(); // every wave is past its last fragment read and load
   TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = i * 32 + (el & 31);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 16 * i + (el & 15);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
+      float x[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float x[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = acc[i][j][4 * g + e];
-          if constexpr (EPI)
-            x[e] = epi_apply1(x[e], bv[j][g][e], ea);
-        }
-        u32x2 v;
-        v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
-        v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
-        const int chunk = (4 * j + g) ^ (r & 15);
-        const int half = ehalf ^ ((r >> 4) & 1);
-        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+      for (int e = 0; e < 4; ++e) {
+        x[e] = acc[i][j][e];
+        if constexpr (EPI)
+          x[e] = epi_apply1(x[e], bv[j][e], ea);
       }
-      __builtin_amdgcn_sched_barrier(0);
+      u32x2 v;
+      v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
+      v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
+      const int chunk = (2 * j + (el >> 5)) ^ (r & 15);
+      *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + ((el >> 4) & 1) * 8) = v;
+      if (j & 1)
+        __builtin_amdgcn_sched_barrier(0);
     }
   }
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
@@ -500,9 +519,7 @@ __device__ __forceinline__ void wide4_tile(const GemmParams &p, int m0, int n0, 
 #pragma unroll
   for (int t = 0; t < 32; ++t) {
     const int r = t * 4 + (el >> 4);
-    u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
-    if ((r >> 4) & 1)
-      v = (u32x4){v[2], v[3], v[0], v[1]};
+    const u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
     const uint32_t off = ((uint32_t)(m0 + wm * 128 + r) * (uint32_t)p.ldc +
                           (uint32_t)(n0 + wn * 128 + 8 * q)) * 2u;
     __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
@@ -1086,12 +1103,10 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   }
 }
 
-// The exact-shape kernel of the 4-wave 256x256x64 2-stage f16 instance: the
-// launcher runs it instead of gemm_kernel when M, N, K are whole tiles and
-// the order is tile, grouped or persistent (GemmParams::exact). A kernel of
-// its own, so that its register allocation is not the general loop's.
+// The 16x16x32 instance of the 4-wave 256x256x64 2-stage f16 configuration
+// (whole tiles; tile, grouped or persistent order).
 template <bool EPI>
-__global__ __launch_bounds__(256, 1) void gemm_wide4(GemmParams p) {
+__global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
   __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
@@ -1105,18 +1120,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide4(GemmParams p) {
     map_program(p, work, tile_m, tile_n, part);
     if (work != prog)
       __syncthreads(); // every wave read its staged epilogue back
-    wide4_tile<EPI>(p, tile_m * 256, tile_n * 256, lds);
+    mfma16_tile<EPI>(p, tile_m * 256, tile_n * 256, lds);
   }
-}
-
-// The exact-shape kernel of an instance, or nullptr.
-template <int BM, int BN, int BK, int WGM, int WGN, int OUT, int ST, bool EPI>
-inline const void *exact_kernel() {
-  if constexpr (BM == 256 && BN == 256 && BK == 64 && WGM == 2 && WGN == 2 && ST == 2 &&
-                OUT == kOutF16)
-    return reinterpret_cast<const void *>(&gemm_wide4<EPI>);
-  else
-    return nullptr;
 }
 
 } // namespace tbk
@@ -1126,8 +1131,7 @@ inline const void *exact_kernel() {
   {{BM, BN, BK, WGM, WGN, OUT, ST, 0},                                           \
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST>),                        \
-   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT, \
-   tbk::exact_kernel<BM, BN, BK, WGM, WGN, OUT, ST, false>()}
+   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT}
 
 #define TBK_OUTS(BM, BN, BK, WGM, WGN, ST)                                      \
   TBK_ENTRY(BM, BN, BK, WGM, WGN, 0, ST), TBK_ENTRY(BM, BN, BK, WGM, WGN, 1, ST), \
@@ -1141,8 +1145,7 @@ inline const void *exact_kernel() {
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST, -1, true>),              \
    "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT \
-   "_epi",                                                                       \
-   tbk::exact_kernel<BM, BN, BK, WGM, WGN, OUT, ST, true>()}
+   "_epi"}
 
 #define TBK_EPI_OUTS(BM, BN, BK, WGM, WGN, ST)                                  \
   TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 0, ST),                                   \

@@ -4,7 +4,11 @@
 #include "gemm_tiles.h"
 
 namespace tbk {
-static const KernelEntry kLargeEpi[] = {TBK_TILES_LARGE(TBK_EPI_OUTS)};
+static const KernelEntry kLargeEpi[] = {
+    TBK_TILES_LARGE(TBK_EPI_OUTS),
+    {{256, 256, 64, 2, 2, kOutF16, 2, 1, 1},
+     reinterpret_cast<const void *>(&gemm_mfma16<true>),
+     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi"}};
 const KernelEntry *entries_large_epi(int *n) {
   *n = sizeof(kLargeEpi) / sizeof(kLargeEpi[0]);
   return kLargeEpi;

@@ -417,6 +417,8 @@ void lowerToGfx950(Module &m, const PassOptions &) {
         {"group_m", I64(g.group_m)}, {"split_k", I64(g.split_k)},
         {"reduction", I64(g.reduction)}, {"num_programs", I64(g.num_programs)},
         {"xcd_remap", I64(g.xcd_remap)}};
+    if (g.mfma != TB_MFMA_32X32X16)
+      cfg["mfma"] = I64(g.mfma);
     if (g.epi_bias || g.epi_activation || g.epi_clamp) {
       cfg["epi_bias"] = I64(g.epi_bias);
       cfg["epi_activation"] = I64(g.epi_activation);
@@ -652,7 +654,10 @@ tb_gemm_config launchConfigOf(const Op &launch) {
   g.reduction = (int32_t)getI64(c, "reduction");
   g.num_programs = getI64(c, "num_programs");
   g.xcd_remap = (int32_t)getI64(c, "xcd_remap");
-  // fused epilogue fields are printed only when some step is requested
+  // the MFMA kind is printed only for 16x16x32, the fused epilogue fields
+  // only when some step is requested
+  if (has(c, "mfma"))
+    g.mfma = (int32_t)getI64(c, "mfma");
   if (has(c, "epi_bias")) {
     g.epi_bias = (int32_t)getI64(c, "epi_bias");
     g.epi_activation = (int32_t)getI64(c, "epi_activation");
@@ -678,10 +683,10 @@ std::string kernelInstanceName(const tb_gemm_config &c) {
   const bool epi = (c.epi_bias || c.epi_activation || c.epi_clamp) &&
                    c.mapping != TB_MAP_SPLIT_K;
   char buf[128];
-  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d%s",
+  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d%s%s",
            (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
            (long long)c.wave_grid_m, (long long)c.wave_grid_n, (long long)c.stages,
-           out, epi ? "_epi" : "");
+           out, c.mfma == TB_MFMA_16X16X32 ? "_16x16x32" : "", epi ? "_epi" : "");
   return buf;
 }
 

@@ -242,6 +242,9 @@ tb_gemm_config lowerContractToConfig(const KernelContract &k) {
   g.epi_clamp = (r.hasMin ? TB_CLAMP_MIN : 0) | (r.hasMax ? TB_CLAMP_MAX : 0);
   g.clamp_min = r.hasMin ? (float)r.clampMin : 0.0f;
   g.clamp_max = r.hasMax ? (float)r.clampMax : 0.0f;
+  g.mfma = c.mmaKind == MmaKind::Mfma16x16x32F16 ? TB_MFMA_16X16X32 : TB_MFMA_32X32X16;
+  if (g.mfma == TB_MFMA_16X16X32 && g.mapping == TB_MAP_SPLIT_K)
+    throw Error("mma = `mfma_f32_16x16x32_f16` has no split-k instance");
   return g;
 }
 

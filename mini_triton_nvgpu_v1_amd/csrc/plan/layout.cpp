@@ -147,9 +147,12 @@ EncodingPlan deriveEncodingPlan(const KernelConfig &c, const TargetInfo &t,
       throw Error("layout freeze requires zero-offset, statically strided operands "
                   "with unit stride on the minor dimension");
   }
-  const int64_t iM = t.mmaInstrShape[0], iN = t.mmaInstrShape[1],
-                iK = t.mmaInstrShape[2];
-  auto [gm, gn] = deriveWaveGrid(c, iM, iN);
+  // the wave grid is chosen on 32x32 MFMA tiles whatever the instruction,
+  // so both instructions see the same wave tiles
+  auto [gm, gn] = deriveWaveGrid(c, t.mmaInstrShape[0], t.mmaInstrShape[1]);
+  const I64s instr = c.mmaKind == MmaKind::Mfma16x16x32F16 ? I64s{16, 16, 32}
+                                                           : t.mmaInstrShape;
+  const int64_t iM = instr[0], iN = instr[1], iK = instr[2];
   const int64_t wtM = c.blockM / gm, wtN = c.blockN / gn;
   const int64_t elem = scalarBytes(c.aScalar);
   const int64_t lanes = t.threadsPerWarp;
@@ -173,7 +176,7 @@ EncodingPlan deriveEncodingPlan(const KernelConfig &c, const TargetInfo &t,
   AttrP mfma = Dialect("amd_mfma", {{"versionMajor", IntU(4)},
                                     {"versionMinor", IntU(0)},
                                     {"warpsPerCTA", IntList({gm, gn})},
-                                    {"instrShape", IntList(t.mmaInstrShape)},
+                                    {"instrShape", IntList(instr)},
                                     {"isTransposed", Bool(true)},
                                     {"cga", cga}});
   auto add = [&](const std::string &name, AttrP a) {

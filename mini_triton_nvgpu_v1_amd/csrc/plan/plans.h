@@ -85,6 +85,7 @@ struct KernelConfig {
              cScalar = ScalarKind::F32;
 };
 const char *scalarName(ScalarKind k);
+bool mfma16x16x32Supported(const KernelConfig &c);
 const char *mmaKindName(MmaKind k);
 int64_t scalarBytes(ScalarKind k);
 KernelConfig getKernelConfig(const Module &m, const Op &matmul);

@@ -156,6 +156,17 @@ static int64_t opI64(const Op &op, const char *name, bool required, int64_t dflt
   return it->second->i;
 }
 
+// gfx950: the v_mfma_f32_16x16x32_f16 instance exists for the 4-wave
+// 256x256x64 2-stage tile with f16 C on whole tiles (the plan's 2x2 wave
+// grid of 128x128 wave tiles). Per FLOP it moves a quarter of the
+// accumulator register traffic of 32x32x16, which this power-limited part
+// turns into a higher sustained clock.
+bool mfma16x16x32Supported(const KernelConfig &c) {
+  return c.blockM == 256 && c.blockN == 256 && c.blockK == 64 && c.numWarps == 4 &&
+         c.requestedStages == 2 && c.cScalar == ScalarKind::F16 &&
+         c.problemM % 256 == 0 && c.problemN % 256 == 0 && c.problemK % 64 == 0;
+}
+
 // Reference: KernelConfig.cpp:86-132 (tb.matmul) and the post-cleanup
 // derivation from module attrs + semantic/mapping plans.
 KernelConfig getKernelConfig(const Module &m, const Op &op) {
@@ -186,11 +197,20 @@ KernelConfig getKernelConfig(const Module &m, const Op &op) {
     if (et == op.attrs.end() || et->second->kind != AttrKind::Bool)
       throw Error("tb.matmul requires bool `exact_tile`");
     k.exactTile = et->second->b;
+    // `mma` names the instruction; without it the plan takes 16x16x32
+    // wherever that instance exists (no split-K: its partials are f32 planes
+    // of the general loop), else 32x32x16
+    const bool splitK = moduleI64(m, kSplitK, false, 1) > 1;
     auto mma = op.attrs.find("mma");
     if (mma != op.attrs.end()) {
       if (mma->second->kind != AttrKind::String)
         throw Error("`mma` must be a string attribute");
       k.mmaKind = enumFromName<MmaKind>(mma->second->s, "mma");
+      if (k.mmaKind == MmaKind::Mfma16x16x32F16 && splitK)
+        throw Error("mma = `mfma_f32_16x16x32_f16` has no split-k instance");
+    } else {
+      k.mmaKind = mfma16x16x32Supported(k) && !splitK ? MmaKind::Mfma16x16x32F16
+                                                       : MmaKind::Mfma32x32x16F16;
     }
   } else {
     MatmulSemantics s = parseMatmulSemanticsAttr(opAttr(op, "tb.semantic_matmul"));
@@ -217,8 +237,12 @@ KernelConfig getKernelConfig(const Module &m, const Op &op) {
 void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t) {
   if (c.aScalar != ScalarKind::F16 || c.bScalar != ScalarKind::F16)
     throw Error("gfx950 stage1 supports fp16 x fp16 -> fp16/fp32 matmul kernels");
-  if (c.mmaKind != MmaKind::Mfma32x32x16F16)
-    throw Error("gfx950 stage1 supports mma = `mfma_f32_32x32x16_f16`");
+  if (c.mmaKind != MmaKind::Mfma32x32x16F16 && c.mmaKind != MmaKind::Mfma16x16x32F16)
+    throw Error("gfx950 stage1 supports mma = `mfma_f32_32x32x16_f16` or "
+                "`mfma_f32_16x16x32_f16`");
+  if (c.mmaKind == MmaKind::Mfma16x16x32F16 && !mfma16x16x32Supported(c))
+    throw Error("mma = `mfma_f32_16x16x32_f16` is implemented for the 4-wave "
+                "256x256x64 2-stage tile with f16 C on whole tiles only");
   if (c.problemM <= 0 || c.problemN <= 0 || c.problemK <= 0)
     throw Error("problem M/N/K must be positive");
   if (c.blockM <= 0 || c.blockN <= 0 || c.blockK <= 0)

@@ -86,6 +86,13 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
                 "accumulates partial sums into C");
   if (c.group_m < 1)
     return fail("group_m must be >= 1");
+  if (c.mfma != TB_MFMA_32X32X16 && c.mfma != TB_MFMA_16X16X32)
+    return fail("mfma must be TB_MFMA_32X32X16 or TB_MFMA_16X16X32");
+  if (c.mfma == TB_MFMA_16X16X32 &&
+      (c.m % c.block_m || c.n % c.block_n || c.k % c.block_k ||
+       c.mapping == TB_MAP_SPLIT_K))
+    return fail("the 16x16x32 instance runs whole tiles only (M, N multiples of "
+                "block_m, block_n, K of block_k) and no split-K");
   const int64_t tiles_m = ceil_div(c.m, c.block_m);
   const int64_t tiles_n = ceil_div(c.n, c.block_n);
   const int64_t tiles_k = ceil_div(c.k, c.block_k);
@@ -146,16 +153,17 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
   const int epi = fused && c.mapping != TB_MAP_SPLIT_K ? 1 : 0;
   tbk::KernelKey key{(int)c.block_m, (int)c.block_n, (int)c.block_k,
                      (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode,
-                     (int)c.stages, epi};
+                     (int)c.stages, epi, (int)c.mfma};
   const tbk::KernelEntry *e = tbk::find_kernel(key);
   if (!e) {
     char buf[256];
     snprintf(buf, sizeof buf,
              "no gfx950 kernel instance for tile %lldx%lldx%lld, wave grid "
-             "%lldx%lld, %lld LDS stages, output mode %d%s",
+             "%lldx%lld, %lld LDS stages, output mode %d%s%s",
              (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
              (long long)c.wave_grid_m, (long long)c.wave_grid_n,
-             (long long)c.stages, out_mode, epi ? " with fused epilogue steps" : "");
+             (long long)c.stages, out_mode, epi ? " with fused epilogue steps" : "",
+             c.mfma == TB_MFMA_16X16X32 ? " on mfma_f32_16x16x32_f16" : "");
     return fail(buf);
   }
   tb_gemm_desc *d = new tb_gemm_desc();
@@ -259,8 +267,6 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
   p.total_work = (int)d->total_work;
   p.xcds = cf.xcd_remap;
   p.ws_ld = (int)cf.n;
-  p.exact = cf.m % cf.block_m == 0 && cf.n % cf.block_n == 0 && cf.k % cf.block_k == 0 &&
-            cf.k > 0 && cf.mapping != TB_MAP_SPLIT_K;
   p.bias = bias;
   p.epi_bias = cf.epi_bias;
   p.epi_act = cf.epi_activation;
@@ -274,8 +280,7 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   void *args[] = {&p};
   const dim3 grid((unsigned)cf.num_programs), block((unsigned)(cf.num_waves * 64));
-  const void *fn = p.exact && d->entry->fn_exact ? d->entry->fn_exact : d->entry->fn;
-  if (int rc = check_hip(hipLaunchKernel(fn, grid, block, args, 0, s),
+  if (int rc = check_hip(hipLaunchKernel(d->entry->fn, grid, block, args, 0, s),
                          "hipLaunchKernel(gemm)"))
     return rc;
   if (cf.mapping == TB_MAP_SPLIT_K && cf.reduction == TB_RED_WORKSPACE) {

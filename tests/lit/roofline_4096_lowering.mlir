@@ -2,7 +2,8 @@
 
 // The roofline configuration: 4096^3 f16 -> f16, 256x256x64 tiles,
 // GROUP_M = 8, 4 waves (a 2x2 wave grid of 128x128 wave tiles): 256 programs,
-// one per CU, in XCD-aware program order.
+// one per CU, in XCD-aware program order. No `mma` attribute: whole tiles of
+// this configuration take v_mfma_f32_16x16x32_f16 (mfma = 1).
 module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {
   func.func @kernel(%A: memref<4096x4096xf16>, %B: memref<4096x4096xf16>,
                     %C: memref<4096x4096xf16>) {
@@ -24,7 +25,8 @@ module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {
 // CHECK-SAME: block = array<i64: 256, 1, 1>
 // CHECK-SAME: group_m = 8 : i64
 // CHECK-SAME: mapping = 1 : i64
+// CHECK-SAME: mfma = 1 : i64
 // CHECK-SAME: num_programs = 256 : i64
 // CHECK-SAME: xcd_remap = 8 : i64
-// CHECK-SAME: kernel = "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
+// CHECK-SAME: kernel = "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
 // CHECK-SAME: lds_bytes = 131072 : i64

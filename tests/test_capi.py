@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirror of tb_gemm_config matches the C compiler's layout."""
-    assert tb.lib().tb_abi_version() == 2
+    assert tb.lib().tb_abi_version() == 3
     fields = [name for name, _ in tb.GemmConfig._fields_]
     src = tmp_path / "layout.c"
     src.write_text(
@@ -52,6 +52,39 @@ def test_kernel_registry_names():
     names = tb.kernel_names()
     assert len(names) >= 40
     assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0" in names
+    assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32" in names
+    assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi" in names
+
+
+def _wide(**kw):
+    c = configs.ROOFLINE.direct_config()
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def test_mfma_16x16x32_instance_selection():
+    """The 4-wave 256x256x64 f16 config binds the 16x16x32 instance when the
+    config asks for it; 32x32x16 stays available for the same tile."""
+    assert configs.ROOFLINE.direct_config().mfma == tb.MFMA_16X16X32
+    d16 = tb.GemmDesc.from_config(_wide())
+    assert d16.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
+    d32 = tb.GemmDesc.from_config(_wide(mfma=tb.MFMA_32X32X16))
+    assert d32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
+    fused = tb.GemmDesc.from_config(_wide(epi_activation=tb.ACT_RELU))
+    assert fused.kernel_name.endswith("_16x16x32_epi")
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(mfma=2), "TB_MFMA_"),
+    (dict(m=4096 - 8), "whole tiles"),
+    (dict(k=4096 - 32, lda=4096 - 32), "whole tiles"),
+    (dict(stages=3), "no gfx950 kernel instance.*16x16x32"),
+    (dict(c_dtype=tb.DTYPE_F32), "no gfx950 kernel instance.*16x16x32"),
+])
+def test_mfma_16x16x32_validation(kw, msg):
+    with pytest.raises(tb.TbError, match=msg):
+        tb.GemmDesc.from_config(_wide(**kw))
 
 
 @pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)

@@ -139,13 +139,17 @@ def test_ragged_edges(M, N, K, tile, device):
 def _every_instance():
     seen = set()
     for name in tb.kernel_names():
-        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{STAGES}_out{OUT}[_epi]
+        # tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{STAGES}_out{OUT}[_16x16x32][_epi]
         body = name[len("tb_gemm_gfx950_"):]
         epi = body.endswith("_epi")
-        shape, waves, stages, out = body[:-4 if epi else None].split("_")
+        body = body[:-4] if epi else body
+        mfma16 = body.endswith("_16x16x32")
+        body = body[:-len("_16x16x32")] if mfma16 else body
+        shape, waves, stages, out = body.split("_")
         bm, bn, bk = map(int, shape.split("x"))
         wgm, wgn = map(int, waves[1:].split("x"))
-        seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:]), int(epi)))
+        seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:]), int(epi),
+                  int(mfma16)))
     return sorted(seen)
 
 
@@ -159,15 +163,19 @@ EPI_STEPS = {0: (tb.EPI_BIAS_F16, tb.ACT_GELU_TANH, 3, -0.5, 1.5),
 @pytest.mark.parametrize("inst", _every_instance(), ids=lambda t: "x".join(map(str, t)))
 def test_every_instance(inst, device):
     """Each compiled instance on a shape with several K tiles (more than the
-    stage count, plus a ragged last tile when possible) and an M/N edge."""
-    bm, bn, bk, wgm, wgn, stages, out, epi = inst
+    stage count, plus a ragged last tile when possible) and an M/N edge; the
+    16x16x32 instance (whole tiles only) on 2x2 tiles and 5 k-tiles."""
+    bm, bn, bk, wgm, wgn, stages, out, epi, mfma16 = inst
     M, N, K = bm + 40, bn * 2 - 24, bk * 5 + (bk // 2 if out == 0 else 0)
+    if mfma16:
+        M, N, K = 2 * bm, 2 * bn, 5 * bk
     print(f"instance {inst} on {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0200 + bm + bn + bk, oracle.UNIFORM)
     tm, tn = -(-M // bm), -(-N // bn)
     kw = dict(m=M, n=N, k=K, lda=K, ldb=N, ldc=N, block_m=bm, block_n=bn,
               block_k=bk, num_waves=wgm * wgn, wave_grid_m=wgm, wave_grid_n=wgn,
-              stages=stages, group_m=8, xcd_remap=0)
+              stages=stages, group_m=8, xcd_remap=0,
+              mfma=tb.MFMA_16X16X32 if mfma16 else tb.MFMA_32X32X16)
     rng = np.random.default_rng(out)
     init = None
     if out == 0:
@@ -207,7 +215,7 @@ def test_every_instance(inst, device):
     cfg.epi_bias, cfg.epi_activation, cfg.epi_clamp = kind, act, bits
     cfg.clamp_min, cfg.clamp_max = lo, hi
     desc = tb.GemmDesc.from_config(cfg)
-    assert desc.kernel_name.endswith(f"_out{out}_epi")
+    assert desc.kernel_name.endswith(f"_out{out}{'_16x16x32' if mfma16 else ''}_epi")
     bias = oracle.fill_f16(1, N, 0x5EED0300 + N, oracle.UNIFORM, 1.0).reshape(N)
     if kind == tb.EPI_BIAS_F32:
         bias = bias.astype(np.float32)

@@ -157,6 +157,14 @@ ERRORS = [
         '"tb.reduction-mode" = "split_k_parallel"'),
      FULL, "needs an f32 C"),
     ("wave_grid", matmul_module(warps=3), FULL, "legal wave grid"),
+    ("mfma16_small_tile", matmul_module(extra_op=', mma = "mfma_f32_16x16x32_f16"'),
+     FULL, "implemented for the 4-wave 256x256x64 2-stage tile"),
+    ("mfma16_split_k", matmul_module(
+        M=256, N=256, K=256, bm=256, bn=256, bk=64,
+        extra_module=', "tb.split-k" = 2 : i64',
+        extra_op=', mma = "mfma_f32_16x16x32_f16"'),
+     FULL, "has no split-k instance"),
+    ("bad_mma", matmul_module(extra_op=', mma = "mfma_f64"'), FULL, "mma"),
     ("f32_a", matmul_module().replace("memref<64x32xf16>", "memref<64x32xf32>"),
      FULL, "fp16 x fp16"),
     ("n_not_8", matmul_module(N=68, exact=False), FULL, "multiples of 8"),
@@ -180,6 +188,25 @@ def test_diagnostics(name, text, arg, msg):
 def test_plan_from_mlir_diagnostics(name, text, arg, msg):
     with pytest.raises(tb.TbError, match=re.escape(msg)):
         tb.plan_from_mlir(text)
+
+
+def test_mfma_instruction_choice():
+    """Without an `mma` attribute the plan takes 16x16x32 exactly where that
+    instance exists: the 4-wave 256x256x64 2-stage f16 tile on whole tiles
+    without split-K. The EncodingPlan records the instruction shape."""
+    def launch(text):
+        return tb.plan_from_mlir(text)
+    wide = dict(M=512, N=768, K=192, bm=256, bn=256, bk=64)
+    assert launch(matmul_module(**wide)).config.mfma == tb.MFMA_16X16X32
+    for kw in (dict(wide, warps=8), dict(wide, bk=32), dict(wide, c="f32"),
+               dict(wide, M=520, exact=False),
+               dict(wide, extra_module=', "tb.split-k" = 3 : i64'),
+               dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"'), {}):
+        assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_32X32X16, kw
+    text = tb_opt(matmul_module(**wide), f"--pass-pipeline={MAINLINE}").stdout
+    assert "instrShape = [16, 16, 32]" in text
+    text = tb_opt(matmul_module(), f"--pass-pipeline={MAINLINE}").stdout
+    assert "instrShape = [32, 32, 16]" in text
 
 
 def test_verifier_catches_tampering():

@@ -1,19 +1,20 @@
-"""GPU parity of the exact-shape kernel of the 4-wave 256x256x64 instance.
+"""GPU parity of the 16x16x32 instance of the 4-wave 256x256x64 tile.
 
-When M and N are multiples of 256 and K of 64 (tile, grouped or persistent
-order), the launcher runs a kernel of its own for the
-`256x256x64_w2x2_s2_out0[_epi]` instance: one wave per SIMD, 128x128 wave
-tiles, the same LDS ring and MFMA k order as the general loop. Two checks:
+`256x256x64_w2x2_s2_out0_16x16x32[_epi]` runs whole tiles (M and N multiples
+of 256, K of 64; tile, grouped or persistent order) with one wave per SIMD,
+128x128 wave tiles and v_mfma_f32_16x16x32_f16, on the same LDS ring as the
+general loop. Checks:
 
 * against the fp64 oracle, |got - ref| <= 1e-2 * (|ref| + 1), on shapes that
   cover 1, 2, odd and even k-tile counts, tile / grouped / persistent orders
   (more tiles than programs), padded leading dimensions and the fused steps;
-* bit-identity with the 8-wave instance (`w4x2`), which runs the general
-  loop: both issue the same MFMAs over the same fragments in the same k
-  order, so C agrees to the last bit.
+* bit-identity with the general loop at 8 waves (`w4x2`) and at 4 waves
+  (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
+  products in the same k order (in 32x32x16 or 16x16x32 steps), and the
+  test pins that the two MFMA shapes round it alike.
 
-Ragged shapes on the same instance take the general loop and are covered by
-test_gemm_gpu.py (test_ragged_edges, test_every_instance).
+Ragged shapes take the general loop (test_gemm_gpu.py: test_ragged_edges,
+test_every_instance).
 """
 import numpy as np
 import pytest
@@ -26,7 +27,7 @@ pytestmark = pytest.mark.gpu
 RTOL = 1e-2
 
 
-def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0):
+def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0, mfma16=False):
     wgm, wgn = (2, 2) if waves == 4 else (4, 2)
     tm, tn = M // 256, N // 256
     return tb.GemmConfig(
@@ -34,7 +35,8 @@ def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0):
         c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, block_m=256, block_n=256,
         block_k=64, num_waves=waves, wave_grid_m=wgm, wave_grid_n=wgn, stages=2,
         mapping=mapping, group_m=8 if mapping != tb.MAP_TILE else 1, split_k=1,
-        reduction=tb.RED_NONE, num_programs=programs or tm * tn, xcd_remap=xcd)
+        reduction=tb.RED_NONE, num_programs=programs or tm * tn, xcd_remap=xcd,
+        mfma=tb.MFMA_16X16X32 if mfma16 else tb.MFMA_32X32X16)
 
 
 def _run(cfg, A, B, device, ld_pad=0, bias=None):
@@ -66,23 +68,26 @@ CASES = [
 @pytest.mark.parametrize("M,N,K,mapping,programs,pad,xcd", CASES,
                          ids=[f"{c[0]}x{c[1]}x{c[2]}_map{c[3]}_p{c[4]}_pad{c[5]}"
                               for c in CASES])
-def test_wide_exact_matches_oracle_and_8_waves(M, N, K, mapping, programs, pad, xcd,
+def test_mfma16_matches_oracle_and_general_loop(M, N, K, mapping, programs, pad, xcd,
                                                device):
     print(f"wide {M}x{N}x{K} mapping {mapping} programs {programs} pad {pad}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0700 + M + K, oracle.NORMAL)
-    name4, got4 = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd), A, B, device, pad)
-    assert name4 == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
-    got4 = got4[:, :N]
+    name16, got16 = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd, mfma16=True),
+                         A, B, device, pad)
+    assert name16 == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
+    got16 = got16[:, :N]
     ref = oracle.gemm_f64(A, B)
-    bad, err, worst = oracle.check_tolerance(got4, ref, rtol=RTOL)
-    print(f"  4 waves: violations={bad} max|err|={err:.3e}", flush=True)
+    bad, err, worst = oracle.check_tolerance(got16, ref, rtol=RTOL)
+    print(f"  16x16x32: violations={bad} max|err|={err:.3e}", flush=True)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
-    _, got8 = _run(_cfg(M, N, K, 8, mapping, programs, pad, xcd), A, B, device, pad)
-    assert np.array_equal(got4.view(np.uint16), got8[:, :N].view(np.uint16))
+    for waves in (8, 4):
+        name, got = _run(_cfg(M, N, K, waves, mapping, programs, pad, xcd), A, B, device, pad)
+        assert "16x16x32" not in name
+        assert np.array_equal(got16.view(np.uint16), got[:, :N].view(np.uint16)), name
 
 
-def test_wide_exact_fused_steps(device):
-    """Bias (f32), tanh GELU and a clamp on the exact-shape kernel, against the
+def test_mfma16_fused_steps(device):
+    """Bias (f32), tanh GELU and a clamp on the 16x16x32 instance, against the
     oracle's epilogue, and bit-identical to the 8-wave fused instance."""
     M, N, K = 512, 768, 192
     print(f"wide fused {M}x{N}x{K}", flush=True)
@@ -90,11 +95,11 @@ def test_wide_exact_fused_steps(device):
     bias = oracle.fill_f16(1, N, 0x5EED0711, oracle.UNIFORM, 1.0).reshape(N).astype(np.float32)
     outs = []
     for waves in (4, 8):
-        cfg = _cfg(M, N, K, waves, tb.MAP_GROUPED_TILE)
+        cfg = _cfg(M, N, K, waves, tb.MAP_GROUPED_TILE, mfma16=waves == 4)
         cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F32, tb.ACT_GELU_TANH
         cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = tb.CLAMP_MIN | tb.CLAMP_MAX, -0.25, 3.0
         name, got = _run(cfg, A, B, device, bias=bias)
-        assert name.endswith("_out0_epi")
+        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), 2, 3, -0.25, 3.0)
