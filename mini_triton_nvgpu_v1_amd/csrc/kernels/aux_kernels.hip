@@ -36,8 +36,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ReduceArgs a) {
   if (a.load_c && !a.c_f16)
     s = *reinterpret_cast<const f32x4 *>(reinterpret_cast<float *>(a.C) +
                                           (size_t)row * a.ldc + col);
-  for (int p = 0; p < a.split_k; ++p) // fixed order: deterministic result
-    s += src[p * (plane / 4)];
+  // fixed order p = 0, 1, ...: deterministic result. The planes are loaded 8
+  // at a time before they are added, so a thread waits for memory once per 8
+  // planes, not once per plane.
+  for (int p0 = 0; p0 < a.split_k; p0 += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (p0 + q < a.split_k)
+        v[q] = src[(p0 + q) * (plane / 4)];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (p0 + q < a.split_k)
+        s += v[q];
+  }
   if (a.epi.bias_kind | a.epi.act | a.epi.clamp) { // fused steps on the whole sum
     const f32x4 b = epi_load_bias(a.epi, col, a.N);
     for (int r = 0; r < 4; ++r)

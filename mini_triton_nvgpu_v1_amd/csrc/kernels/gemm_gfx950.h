@@ -114,6 +114,19 @@ __device__ __forceinline__ epi_f32x4 epi_load_bias(const EpiArgs &e, int col, in
   return b;
 }
 
+// The same steps with the activation fixed at compile time and the clamps as
+// selects against bounds that are -inf / +inf when a clamp is off (the same
+// comparisons as epi_apply1, so the same results, NaN included): no branch
+// per element in unrolled epilogue loops.
+template <int ACT>
+__device__ __forceinline__ float epi_apply_t(float x, float bias, float lo, float hi) {
+  x += bias;
+  x = epi_activation(x, ACT);
+  x = x < lo ? lo : x;
+  x = x > hi ? hi : x;
+  return x;
+}
+
 __device__ __forceinline__ float epi_apply1(float x, float bias, const EpiArgs &e) {
   x += bias;
   x = epi_activation(x, e.act);

@@ -279,9 +279,11 @@ __device__ __forceinline__ void sched_step() {
 // + r], r = 0..3. Slot schedule per 32-deep k step (64 MFMAs, m = 8ii + jj):
 // the reads of the next k step in the order A0, B0 (two halves) .. B7, A1 ..
 // A7, op o in slot 8o/3; the barrier before slot 40 of the last k step; after
-// it the next k-tile's first reads (op o in slot 40 + o) and its refill
-// (loads 0..7 in the even slots 40..54, 8..15 in the odd slots 1..15 of the
-// next k-tile).
+// it the next k-tile's first reads (op o in slot 40 + o) and its refill, one
+// load every 4 slots (loads 0..5 in slots 40..60, 6..15 in slots 0..36 of the
+// next k-tile): a CU then asks the L2 for 64 KiB over ~1000 cycles, about
+// what the L2 -> CU path sustains. Bunched into 40 slots, the queued loads
+// held up the lone wave's issue (1% slower).
 template <bool EPI>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
   constexpr int BK = 64, BQ = 40;
@@ -448,13 +450,14 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       constexpr int m = BQ + decltype(s_c)::value;
       mfma(1, m, false);
       rd(0, Sn, 0, m - BQ);
-      if constexpr (((m - BQ) & 1) == 0 && m - BQ < 16)
-        load(ra, rb, it + 2, stage, (m - BQ) >> 1);
+      if constexpr (((m - BQ) & 3) == 0)
+        load(ra, rb, it + 2, stage, (m - BQ) >> 2);
       __builtin_amdgcn_sched_barrier(0);
     });
+    constexpr int NB = (64 - BQ) / 4; // refill loads issued before k-tile it+1
     auto refill = [&](int m) {
-      if ((m & 1) && m < 16)
-        load(ra, rb, it + 2, stage, 8 + (m >> 1));
+      if ((m & 3) == 0 && m < 4 * (16 - NB))
+        load(ra, rb, it + 2, stage, NB + (m >> 2));
     };
     kstep0(Sn, refill, false);
     kstep1(Z{}, Q{});
@@ -491,28 +494,45 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   }
   barrier(); // every wave is past its last fragment read and load
   TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
+  // clamp bounds: -inf / +inf for a clamp that is off
+  const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
+  const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
+  auto to_lds = [&](auto act_c) {
+    constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 16 * i + (el & 15);
+    for (int i = 0; i < 8; ++i) {
+      const int r = 16 * i + (el & 15);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float x[4];
+      for (int j = 0; j < 8; ++j) {
+        float x[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        x[e] = acc[i][j][e];
-        if constexpr (EPI)
-          x[e] = epi_apply1(x[e], bv[j][e], ea);
+        for (int e = 0; e < 4; ++e) {
+          x[e] = acc[i][j][e];
+          if constexpr (EPI)
+            x[e] = epi_apply_t<ACT>(x[e], bv[j][e], lo, hi);
+        }
+        u32x2 v;
+        v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
+        v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
+        const int chunk = (2 * j + (el >> 5)) ^ (r & 15);
+        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + ((el >> 4) & 1) * 8) = v;
+        if (j & 1)
+          __builtin_amdgcn_sched_barrier(0);
       }
-      u32x2 v;
-      v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
-      v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
-      const int chunk = (2 * j + (el >> 5)) ^ (r & 15);
-      *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + ((el >> 4) & 1) * 8) = v;
-      if (j & 1)
-        __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  // the activation is dispatched once, not per element
+  if constexpr (EPI) {
+    switch (p.epi_act) {
+    case 1: to_lds(std::integral_constant<int, 1>{}); break;
+    case 2: to_lds(std::integral_constant<int, 2>{}); break;
+    case 3: to_lds(std::integral_constant<int, 3>{}); break;
+    default: to_lds(std::integral_constant<int, 0>{}); break;
+    }
+  } else {
+    to_lds(std::integral_constant<int, 0>{});
   }
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
   const int q = el & 15;
