@@ -182,7 +182,8 @@ def main() -> int:
         for other in configs.ALL + configs.FUSED:
             if other.name == w.name:
                 continue
-            steps = 200 if other.flop < 1e9 else (50 if other.flop < 2e11 else 10)
+            # a few tens of ms of GPU time per extra: long enough for a steady clock
+            steps = 200 if other.flop < 1e9 else (300 if other.flop < 2e11 else 60)
             o = time_workload(other, steps, steps, device)
             us = o["avg_launch_ms"] * 1e3
             wall_us = o["wall_s"] * 1e6 / steps

@@ -877,16 +877,30 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           bv[j][g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
+      // the activation dispatched once (no branch per element); clamp
+      // bounds -inf / +inf for a clamp that is off
+      const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
+      const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
+      auto steps = [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
+        for (int j = 0; j < TN; ++j) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+          for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int g = 0; g < 4; ++g)
+            for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[i][j][4 * g + r] = epi_apply1(acc[i][j][4 * g + r], bv[j][g][r], ea);
-        __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
+              for (int r = 0; r < 4; ++r)
+                acc[i][j][4 * g + r] =
+                    epi_apply_t<ACT>(acc[i][j][4 * g + r], bv[j][g][r], lo, hi);
+          __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
+        }
+      };
+      switch (p.epi_act) {
+      case 1: steps(std::integral_constant<int, 1>{}); break;
+      case 2: steps(std::integral_constant<int, 2>{}); break;
+      case 3: steps(std::integral_constant<int, 3>{}); break;
+      default: steps(std::integral_constant<int, 0>{}); break;
       }
     }
 
