@@ -27,6 +27,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace tbk {
 
 enum MappingKind : int {
@@ -75,24 +77,25 @@ struct EpiArgs {
   float lo, hi;
 };
 
-// x / (1 + e^-z) with the hardware exp2 (v_exp_f32) and reciprocal
-// (v_rcp_f32), each about 1 ulp: e^-z = 2^(-z log2 e). For z -> -inf the
-// denominator is +inf and the result 0; for z -> +inf it is x.
-__device__ __forceinline__ float epi_x_sigmoid(float x, float z) {
-  const float e = __builtin_amdgcn_exp2f(-z * 1.4426950408889634f);
-  return x * __builtin_amdgcn_rcpf(1.f + e);
+// x / (1 + 2^t) with the hardware exp2 (v_exp_f32) and reciprocal
+// (v_rcp_f32), each about 1 ulp; x sigmoid(z) is t = -z log2 e. For t ->
+// +inf the denominator is +inf and the result 0; for t -> -inf it is x.
+__device__ __forceinline__ float epi_x_sigmoid2(float x, float t) {
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
 }
 
 __device__ __forceinline__ float epi_activation(float x, int act) {
   if (act == 1)
     return x > 0.f ? x : 0.f;
   if (act == 2) { // tanh form of GELU (Hendrycks & Gimpel, 2016):
-    // 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
-    const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
-    return epi_x_sigmoid(x, u2);
+    // 0.5 x (1 + tanh(u)) = x sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3);
+    // -2u log2 e = x (a + b x^2), a = -2 sqrt(2/pi) log2 e, b = 0.044715 a
+    // (three operations before the exp2, not five)
+    const float t = x * __builtin_fmaf(-0.1029432395800235f, x * x, -2.302208198144325f);
+    return epi_x_sigmoid2(x, t);
   }
   if (act == 3) // SiLU: x sigmoid(x)
-    return epi_x_sigmoid(x, x);
+    return epi_x_sigmoid2(x, x * -1.4426950408889634f);
   return x;
 }
 
@@ -114,17 +117,44 @@ __device__ __forceinline__ epi_f32x4 epi_load_bias(const EpiArgs &e, int col, in
   return b;
 }
 
-// The same steps with the activation fixed at compile time and the clamps as
-// selects against bounds that are -inf / +inf when a clamp is off (the same
-// comparisons as epi_apply1, so the same results, NaN included): no branch
-// per element in unrolled epilogue loops.
-template <int ACT>
+// The same steps with the activation fixed at compile time and, when CLAMP,
+// the clamps as selects against bounds that are -inf / +inf for a clamp that
+// is off (the same comparisons as epi_apply1, so the same results, NaN
+// included): no branch per element in unrolled epilogue loops, and no
+// compare / select pairs when neither clamp is set.
+template <int ACT, bool CLAMP>
 __device__ __forceinline__ float epi_apply_t(float x, float bias, float lo, float hi) {
   x += bias;
   x = epi_activation(x, ACT);
-  x = x < lo ? lo : x;
-  x = x > hi ? hi : x;
+  if constexpr (CLAMP) {
+    x = x < lo ? lo : x;
+    x = x > hi ? hi : x;
+  }
   return x;
+}
+
+// Calls f(integral_constant<int, ACT>, integral_constant<bool, CLAMP>) once
+// for the activation and clamp a launch carries: the per-tile dispatch of
+// code unrolled over a tile's elements.
+template <typename F>
+__device__ __forceinline__ void epi_dispatch(int act, int clamp, F &&f) {
+  using C0 = std::integral_constant<bool, false>;
+  using C1 = std::integral_constant<bool, true>;
+  if (clamp) {
+    switch (act) {
+    case 1: f(std::integral_constant<int, 1>{}, C1{}); break;
+    case 2: f(std::integral_constant<int, 2>{}, C1{}); break;
+    case 3: f(std::integral_constant<int, 3>{}, C1{}); break;
+    default: f(std::integral_constant<int, 0>{}, C1{}); break;
+    }
+  } else {
+    switch (act) {
+    case 1: f(std::integral_constant<int, 1>{}, C0{}); break;
+    case 2: f(std::integral_constant<int, 2>{}, C0{}); break;
+    case 3: f(std::integral_constant<int, 3>{}, C0{}); break;
+    default: f(std::integral_constant<int, 0>{}, C0{}); break;
+    }
+  }
 }
 
 __device__ __forceinline__ float epi_apply1(float x, float bias, const EpiArgs &e) {

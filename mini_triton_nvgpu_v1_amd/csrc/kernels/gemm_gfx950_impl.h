@@ -92,6 +92,13 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0): also every LDS read of this wave is done.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
 // Program id -> (tile_m, tile_n, split part).
 // tile / grouped / persistent: lib/Transforms/LowerPipelineToNVGPU.cpp:286-305
 // split-K: LowerPipelineToNVGPU.cpp:306-317
@@ -259,10 +266,10 @@ __device__ __forceinline__ void sched_step() {
 //  * no per-load bounds checks: tiles are whole, and the ring's lookahead
 //    loads past the last k-tile use a descriptor of zero records (zeros);
 //  * one loop iteration runs from a k-tile's barrier to the next, so the
-//    fragment reads in flight at the back-edge are consumed already and no
-//    lgkmcnt(0) lands in front of the first MFMAs of a k-tile; the barrier is
-//    vmcnt(0) + s_barrier (every LDS read before it has been consumed by an
-//    MFMA, and the stage it frees is only written by loads issued after it).
+//    compiler's waits for fragment reads never land in front of the first
+//    MFMAs of a k-tile; the barrier is vmcnt(0) lgkmcnt(0) + s_barrier (this
+//    wave's loads have landed and its reads of the stage the barrier frees
+//    have returned; that stage is only written by loads issued after it).
 // The MFMA is inline asm with the accumulator tied in place ("+a"): the
 // builtin's register allocation rotates 16x16 accumulators through copies
 // (dst != srcC), 248 extra moves per two k-tiles. Asm carries no hazard
@@ -280,13 +287,15 @@ __device__ __forceinline__ void sched_step() {
 // the reads of the next k step in the order A0, B0 (two halves) .. B7, A1 ..
 // A7, op o in slot 8o/3; the barrier before slot 40 of the last k step; after
 // it the next k-tile's first reads (op o in slot 40 + o) and its refill, one
-// load every 4 slots (loads 0..5 in slots 40..60, 6..15 in slots 0..36 of the
-// next k-tile): a CU then asks the L2 for 64 KiB over ~1000 cycles, about
+// load every 5 slots (loads 0..4 in slots 40..60, 5..15 in slots 1..51 of the
+// next k-tile): a CU then asks the L2 for 64 KiB over ~1200 cycles, about
 // what the L2 -> CU path sustains. Bunched into 40 slots, the queued loads
-// held up the lone wave's issue (1% slower).
+// held up the lone wave's issue (1% slower); every 4 or 3 slots measured
+// 0.7% and 1.3% slower than every 5, and the barrier at slot 32 or 48 no
+// faster than at 40.
 template <bool EPI>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
-  constexpr int BK = 64, BQ = 40;
+  constexpr int BK = 64, BQ = 40, LS = 5;
   constexpr uint32_t SLOT = 65536; // ring slot: A [256][64] at 0, B [64][256] at 32 KiB
   constexpr uint32_t B_AT = 32768;
   const int lane = threadIdx.x & 63;
@@ -444,20 +453,26 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(p.A, ok ? a_bytes : 0u);
     const u32x4 rb = rsrc_dwords(p.B, ok ? b_bytes : 0u);
-    wait_vmcnt<0>(); // k-tile it+1 landed (this wave's part)
+    // k-tile it+1 landed (this wave's part), and this wave's reads of stage
+    // S are done (the last A rows of k step 1 are read in k step 0 but only
+    // consumed after the barrier, by MFMAs 40..63)
+    wait_vmcnt_lgkm0<0>();
     barrier();
+    static_assert(64 - BQ == 24, "one read op per slot after the barrier");
     static_for<64 - BQ>([&](auto s_c) {
       constexpr int m = BQ + decltype(s_c)::value;
       mfma(1, m, false);
       rd(0, Sn, 0, m - BQ);
-      if constexpr (((m - BQ) & 3) == 0)
-        load(ra, rb, it + 2, stage, (m - BQ) >> 2);
+      if constexpr (((m - BQ) % LS) == 0)
+        load(ra, rb, it + 2, stage, (m - BQ) / LS);
       __builtin_amdgcn_sched_barrier(0);
     });
-    constexpr int NB = (64 - BQ) / 4; // refill loads issued before k-tile it+1
+    constexpr int NB = (64 - BQ + LS - 1) / LS; // refill loads issued before k-tile it+1
+    constexpr int OFF = NB * LS - (64 - BQ);    // slot of k-tile it+1 with its first load
+    static_assert(OFF + (16 - NB - 1) * LS < 64, "refill fits one k-tile");
     auto refill = [&](int m) {
-      if ((m & 3) == 0 && m < 4 * (16 - NB))
-        load(ra, rb, it + 2, stage, NB + (m >> 2));
+      if (m >= OFF && ((m - OFF) % LS) == 0 && NB + (m - OFF) / LS < 16)
+        load(ra, rb, it + 2, stage, NB + (m - OFF) / LS);
     };
     kstep0(Sn, refill, false);
     kstep1(Z{}, Q{});
@@ -497,8 +512,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // clamp bounds: -inf / +inf for a clamp that is off
   const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
   const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
-  auto to_lds = [&](auto act_c) {
+  auto to_lds = [&](auto act_c, auto clamp_c) {
     constexpr int ACT = decltype(act_c)::value;
+    constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 16 * i + (el & 15);
@@ -509,7 +525,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
         for (int e = 0; e < 4; ++e) {
           x[e] = acc[i][j][e];
           if constexpr (EPI)
-            x[e] = epi_apply_t<ACT>(x[e], bv[j][e], lo, hi);
+            x[e] = epi_apply_t<ACT, CLAMP>(x[e], bv[j][e], lo, hi);
         }
         u32x2 v;
         v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
@@ -523,17 +539,11 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       }
     }
   };
-  // the activation is dispatched once, not per element
-  if constexpr (EPI) {
-    switch (p.epi_act) {
-    case 1: to_lds(std::integral_constant<int, 1>{}); break;
-    case 2: to_lds(std::integral_constant<int, 2>{}); break;
-    case 3: to_lds(std::integral_constant<int, 3>{}); break;
-    default: to_lds(std::integral_constant<int, 0>{}); break;
-    }
-  } else {
-    to_lds(std::integral_constant<int, 0>{});
-  }
+  // the activation and clamp are dispatched once, not per element
+  if constexpr (EPI)
+    epi_dispatch(p.epi_act, p.epi_clamp, to_lds);
+  else
+    to_lds(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
   const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
   const int q = el & 15;
 #pragma unroll
@@ -877,12 +887,13 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           bv[j][g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
-      // the activation dispatched once (no branch per element); clamp
-      // bounds -inf / +inf for a clamp that is off
+      // the activation and clamp dispatched once (no branch per element);
+      // clamp bounds -inf / +inf for a clamp that is off
       const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
       const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
-      auto steps = [&](auto act_c) {
+      auto steps = [&](auto act_c, auto clamp_c) {
         constexpr int ACT = decltype(act_c)::value;
+        constexpr bool CLAMP = decltype(clamp_c)::value;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -892,16 +903,11 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
               for (int r = 0; r < 4; ++r)
                 acc[i][j][4 * g + r] =
-                    epi_apply_t<ACT>(acc[i][j][4 * g + r], bv[j][g][r], lo, hi);
+                    epi_apply_t<ACT, CLAMP>(acc[i][j][4 * g + r], bv[j][g][r], lo, hi);
           __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
         }
       };
-      switch (p.epi_act) {
-      case 1: steps(std::integral_constant<int, 1>{}); break;
-      case 2: steps(std::integral_constant<int, 2>{}); break;
-      case 3: steps(std::integral_constant<int, 3>{}); break;
-      default: steps(std::integral_constant<int, 0>{}); break;
-      }
+      epi_dispatch(p.epi_act, p.epi_clamp, steps);
     }
 
     if constexpr (OUT == kOutF16 && T::STAGED_F16_EPILOGUE) {
