@@ -80,8 +80,14 @@ struct EpiArgs {
 // x / (1 + 2^t) with the hardware exp2 (v_exp_f32) and reciprocal
 // (v_rcp_f32), each about 1 ulp; x sigmoid(z) is t = -z log2 e. For t ->
 // +inf the denominator is +inf and the result 0; for t -> -inf it is x.
+// The product is kept as an f32 value (an empty asm on it): otherwise a
+// following f16 cast can be fused with it into one v_fma_mixlo_f16, which
+// rounds the product once to f16, in kernels that cast right away and not in
+// the others, and the kernels' results would differ in the last f16 bit.
 __device__ __forceinline__ float epi_x_sigmoid2(float x, float t) {
-  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
+  float y = x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t));
+  asm("" : "+v"(y));
+  return y;
 }
 
 __device__ __forceinline__ float epi_activation(float x, int act) {

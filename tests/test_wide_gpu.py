@@ -11,7 +11,10 @@ general loop. Checks:
 * bit-identity with the general loop at 8 waves (`w4x2`) and at 4 waves
   (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
   products in the same k order (in 32x32x16 or 16x16x32 steps), and the
-  test pins that the two MFMA shapes round it alike.
+  test pins that the two MFMA shapes round it alike;
+* every compile-time variant of the fused steps (activation x whether a
+  clamp is set), against the oracle and bit-identical between the 16x16x32
+  instance and the general loop's fused instance.
 
 Ragged shapes take the general loop (test_gemm_gpu.py: test_ragged_edges,
 test_every_instance).
@@ -103,6 +106,38 @@ def test_mfma16_fused_steps(device):
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), 2, 3, -0.25, 3.0)
+    bad, err, worst = oracle.check_tolerance(outs[0], ref, rtol=RTOL)
+    print(f"  violations={bad} max|err|={err:.3e}", flush=True)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+
+
+# (activation, clamp bits, lo, hi): every compile-time (activation, clamp)
+# variant of the fused steps, with an f16 bias so that even "no activation,
+# no clamp" runs the fused instance.
+EPI_VARIANTS = [(act, cl, -0.25, 0.5) for act in (0, 1, 2, 3) for cl in (0, 1, 3)]
+
+
+@pytest.mark.parametrize("act,clamp,lo,hi", EPI_VARIANTS,
+                         ids=[f"act{v[0]}_clamp{v[1]}" for v in EPI_VARIANTS])
+def test_fused_step_variants(act, clamp, lo, hi, device):
+    """Each activation with no clamp, a lower clamp and both clamps, on the
+    16x16x32 instance and on the general loop's fused 8-wave instance: both
+    match the oracle's epilogue and are bit-identical to each other."""
+    M, N, K = 512, 512, 128
+    print(f"wide fused variant act {act} clamp {clamp}", flush=True)
+    A, B = oracle.config_inputs(M, N, K, 0x5EED0720 + 4 * act + clamp, oracle.NORMAL)
+    bias = oracle.fill_f16(1, N, 0x5EED0721, oracle.UNIFORM, 1.0).reshape(N)
+    outs = []
+    for waves in (4, 8):
+        cfg = _cfg(M, N, K, waves, tb.MAP_GROUPED_TILE, mfma16=waves == 4)
+        cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F16, act
+        cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = clamp, lo, hi
+        name, got = _run(cfg, A, B, device, bias=bias)
+        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
+        outs.append(got)
+    ref = oracle.gemm_f64(A, B)
+    oracle.epilogue_f64(ref, bias.astype(np.float64), act, clamp, lo, hi)
     bad, err, worst = oracle.check_tolerance(outs[0], ref, rtol=RTOL)
     print(f"  violations={bad} max|err|={err:.3e}", flush=True)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
