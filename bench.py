@@ -114,12 +114,28 @@ def cpu_baseline(w, budget_s: float = 12.0):
             break
     best = min(times)
     med = statistics.median(times)
+    # the same GEMM on one core, over a slab of rows (a few seconds)
+    rows1 = max(1, min(w.M, 256))
+    flop1 = 2.0 * rows1 * w.N * w.K
+    t1 = []
+    t_end = time.perf_counter() + budget_s / 3
+    while time.perf_counter() < t_end or not t1:
+        t0 = time.perf_counter()
+        oracle.gemm_f32(A[:rows1], B, threads=1)
+        t1.append(time.perf_counter() - t0)
+        if len(t1) >= 20:
+            break
+    med1 = statistics.median(t1)
     return {"value": flop / med / 1e12, "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": (f"{len(times)} x fp32 {rows}x{w.N}x{w.K} GEMM on host "
                        f"(oracle tbo_gemm_f32, OpenMP {threads} threads, median "
                        f"{med * 1e3:.1f} ms, best {best * 1e3:.1f} ms); "
-                       f"{os.uname().machine} {cpu_model()}")}
+                       f"{os.uname().machine} {cpu_model()}"),
+            "single_core": {"value": flop1 / med1 / 1e12, "unit": "TFLOP/s", "cores": 1,
+                            "sample": (f"{len(t1)} x fp32 {rows1}x{w.N}x{w.K} GEMM "
+                                       f"(first {rows1} rows), 1 thread, median "
+                                       f"{med1 * 1e3:.1f} ms")}}
 
 
 def cpu_model() -> str:
