@@ -172,7 +172,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
-              "the GEMM shards by output row panels with no exchange, see DESIGN.md",
+              "across GPUs the GEMM would shard by output row panels with no exchange",
               file=sys.stderr)
         return 2
 

@@ -7,7 +7,7 @@ Runs, on one stream and in this order:
   2. `--reps` launches of the workload's GEMM through the C ABI.
 
 Usage (under rocprofv3, the program after `--`):
-  rocprofv3 --pmc FETCH_SIZE -d gpurun_out/p -- \
+  rocprofv3 --pmc FETCH_SIZE -d out/pmc -- \
       python3 -m mini_triton_nvgpu_v1_amd.profiling --workload gemm_4096
 """
 from __future__ import annotations
