@@ -113,6 +113,33 @@ def test_plan_module_f32_accumulate(name, M, N, K, tile, warps, extra, device):
     check(got, A, B, init=C0)
 
 
+# Large shapes with edges in M, N and K, through the plan pipeline: partial
+# 256x256 tiles with a ragged last k-tile, a split-K whose 157 k-tiles do not
+# divide by 8 splits (5 splits take one more), and persistent order over
+# ragged tiles on 7 programs. K, N and the leading dimensions stay multiples
+# of 8, which the C ABI requires.
+LARGE_RAGGED = [
+    configs.Workload("ragged_1000x1496x712", 1000, 1496, 712, 0x5EED0200, configs.NORMAL,
+                     (256, 256, 64), num_waves=4, exact_tile=False),
+    configs.Workload("ragged_splitk_300x520x10000", 300, 520, 10000, 0x5EED0201,
+                     configs.UNIFORM, (128, 64, 64), num_waves=4, stages=3, split_k=8,
+                     exact_tile=False),
+    configs.Workload("ragged_persistent_1300x904x520", 1300, 904, 520, 0x5EED0202,
+                     configs.NORMAL, (256, 256, 64), num_waves=4, persistent=True,
+                     num_ctas=7, exact_tile=False),
+]
+
+
+@pytest.mark.parametrize("w", LARGE_RAGGED, ids=lambda w: w.name)
+def test_large_ragged_parity(w, device):
+    print(f"large ragged {w.name}", flush=True)
+    A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
+    desc = tb.plan_from_mlir(w.mlir())
+    assert "16x16x32" not in desc.kernel_name  # whole tiles only there
+    got = run_desc(desc, A, B, device)
+    check(got, A, B)
+
+
 RAGGED_SHAPES = [(1, 8, 8), (33, 24, 16), (97, 88, 40), (200, 136, 72),
                  (65, 64, 32), (64, 72, 96), (130, 264, 264)]
 
