@@ -14,7 +14,8 @@ general loop. Checks:
   test pins that the two MFMA shapes round it alike;
 * every compile-time variant of the fused steps (activation x whether a
   clamp is set), against the oracle and bit-identical between the 16x16x32
-  instance and the general loop's fused instance.
+  instance and the general loop's fused instance, and the fused instance in
+  persistent order.
 
 Ragged shapes take the general loop (test_gemm_gpu.py: test_ragged_edges,
 test_every_instance).
@@ -138,6 +139,32 @@ def test_fused_step_variants(act, clamp, lo, hi, device):
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), act, clamp, lo, hi)
+    bad, err, worst = oracle.check_tolerance(outs[0], ref, rtol=RTOL)
+    print(f"  violations={bad} max|err|={err:.3e}", flush=True)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+
+
+def test_fused_steps_persistent(device):
+    """The fused 16x16x32 instance in persistent grouped order (9 tiles on 4
+    programs, so a program runs its epilogue, then another tile's main
+    loop): against the oracle and bit-identical to the 8-wave fused
+    instance in plain grouped order."""
+    M, N, K = 768, 768, 192
+    print(f"wide fused persistent {M}x{N}x{K}", flush=True)
+    A, B = oracle.config_inputs(M, N, K, 0x5EED0730, oracle.NORMAL)
+    bias = oracle.fill_f16(1, N, 0x5EED0731, oracle.UNIFORM, 1.0).reshape(N).astype(np.float32)
+    outs = []
+    for waves, mapping, programs in ((4, tb.MAP_PERSISTENT_GROUPED, 4),
+                                     (8, tb.MAP_GROUPED_TILE, None)):
+        cfg = _cfg(M, N, K, waves, mapping, programs, mfma16=waves == 4)
+        cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F32, tb.ACT_SILU
+        cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = tb.CLAMP_MIN, -0.125, 0.0
+        name, got = _run(cfg, A, B, device, bias=bias)
+        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
+        outs.append(got)
+    ref = oracle.gemm_f64(A, B)
+    oracle.epilogue_f64(ref, bias.astype(np.float64), 3, 1, -0.125, 0.0)
     bad, err, worst = oracle.check_tolerance(outs[0], ref, rtol=RTOL)
     print(f"  violations={bad} max|err|={err:.3e}", flush=True)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
