@@ -154,8 +154,10 @@ size_t tb_workspace_bytes(const tb_gemm_desc *desc);
 
 /* Enqueue C = A*B (or C += A*B for TB_ACC_INIT_LOAD_C) on `stream`, then
  * the fused epilogue steps of the config. Fails for a config with a bias
- * (use tb_gemm_launch_ex). Reference: the launcher of the lowered kernel,
- * tools/bench_stage1_fair.py:665-699 (A, B, C device pointers). */
+ * (use tb_gemm_launch_ex). A, B, C and the workspace must be 16-byte aligned
+ * (hipMalloc and torch allocations are). Reference: the launcher of the
+ * lowered kernel, tools/bench_stage1_fair.py:665-699 (A, B, C device
+ * pointers). */
 int tb_gemm_launch(const tb_gemm_desc *desc, const void *a, const void *b,
                    void *c, void *workspace, void *stream);
 

@@ -232,6 +232,10 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
     return fail("tb_gemm_launch: desc is NULL");
   if (!a || !b || !c)
     return fail("tb_gemm_launch: A, B and C must be device pointers");
+  // every kernel moves 16-byte vectors from these bases
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+       reinterpret_cast<uintptr_t>(c)) % 16)
+    return fail("tb_gemm_launch: A, B and C must be 16-byte aligned");
   if (d->cfg.epi_bias != TB_EPI_BIAS_NONE) {
     // the epilogue reads 4 bias values per vector load
     const uintptr_t align = d->cfg.epi_bias == TB_EPI_BIAS_F16 ? 8 : 16;
@@ -246,6 +250,8 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
   if (d->workspace_bytes && !workspace)
     return fail("tb_gemm_launch: this descriptor needs a workspace of " +
                 std::to_string(d->workspace_bytes) + " bytes");
+  if (d->workspace_bytes && reinterpret_cast<uintptr_t>(workspace) % 16)
+    return fail("tb_gemm_launch: the workspace must be 16-byte aligned");
   const tb_gemm_config &cf = d->cfg;
   tbk::GemmParams p{};
   p.A = a;

@@ -139,6 +139,11 @@ def test_launch_argument_errors_before_any_gpu_call():
         d.launch(0, 0, 0)
     with pytest.raises(tb.TbError, match="workspace"):
         d.launch(16, 16, 16, None)
+    for a, b, c in ((18, 16, 16), (16, 24, 16), (16, 16, 20)):
+        with pytest.raises(tb.TbError, match="A, B and C must be 16-byte aligned"):
+            d.launch(a, b, c, 256)
+    with pytest.raises(tb.TbError, match="workspace must be 16-byte aligned"):
+        d.launch(16, 16, 16, 264)
 
 
 def test_fused_epilogue_instances_and_bias_arguments():
