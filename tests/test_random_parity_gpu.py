@@ -1,6 +1,7 @@
 """Randomized GPU parity: 400 seeded random cases over every plain compiled
-instance, every program order and both split-K reductions, each against the
-fp64 oracle (|got - ref| <= 1e-2 * (|ref| + 1)).
+instance, every program order and both split-K reductions, and 200 over the
+fused-step (`_epi`) instances and the split-K reduction's fused steps, each
+against the fp64 oracle (|got - ref| <= 1e-2 * (|ref| + 1)).
 
 A case draws an instance, a shape (M any size, N and K multiples of 8, the C
 ABI's transport rule; whole tiles for the 16x16x32 instance), GROUP_M, the
@@ -78,5 +79,85 @@ def test_random_parity(device):
         bad, err, worst = oracle.check_tolerance(got, ref, rtol=RTOL)
         if bad:
             failures.append(f"case {case} ({desc.kernel_name}): {bad} violations, "
+                            f"worst {err} at {worst}")
+    assert not failures, "\n".join(failures)
+
+
+FUSED_CASES = 200
+
+
+def _fused_case(rng, insts, case):
+    """A random fused-step configuration on an `_epi` instance: f16 C, plain
+    f32 C, f32 C += A*B, or split-K (the steps then run in the reduction)."""
+    bm, bn, bk, wgm, wgn, stages, out, _epi, mfma16 = rng.choice(insts)
+    if mfma16:
+        M, N, K = 256 * rng.randint(1, 2), 256 * rng.randint(1, 3), 64 * rng.randint(1, 8)
+    else:
+        M, N, K = rng.randint(1, 400), 8 * rng.randint(1, 64), 8 * rng.randint(1, 96)
+    tm, tn = -(-M // bm), -(-N // bn)
+    lo = rng.uniform(-1.0, 0.5)
+    steps = dict(epi_bias=rng.choice([tb.EPI_BIAS_NONE, tb.EPI_BIAS_F16, tb.EPI_BIAS_F32]),
+                 epi_activation=rng.choice([tb.ACT_RELU, tb.ACT_GELU_TANH, tb.ACT_SILU]),
+                 epi_clamp=rng.randint(0, 3), clamp_min=lo, clamp_max=lo + rng.uniform(0, 2))
+    kw = dict(m=M, n=N, k=K, lda=K, ldb=N, ldc=N, block_m=bm, block_n=bn, block_k=bk,
+              num_waves=wgm * wgn, wave_grid_m=wgm, wave_grid_n=wgn, stages=stages,
+              group_m=rng.choice([1, 8]), xcd_remap=rng.choice([0, 8]),
+              mfma=tb.MFMA_16X16X32 if mfma16 else tb.MFMA_32X32X16, **steps)
+    mapping = rng.choice(MAPS)
+    progs = tm * tn if mapping in MAPS[:2] else rng.randint(1, tm * tn)
+    init = None
+    if out == 0:
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, mapping=mapping,
+                            split_k=1, reduction=tb.RED_NONE, num_programs=progs, **kw)
+    elif out == 1 and rng.random() < 0.5:  # plain f32 store
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_ZERO,
+                            mapping=tb.MAP_TILE, split_k=1, reduction=tb.RED_NONE,
+                            num_programs=tm * tn, **kw)
+    elif out == 1:  # split-K: the reduction applies the steps
+        s = rng.randint(2, 8)
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO,
+                            mapping=tb.MAP_SPLIT_K, split_k=s, reduction=tb.RED_WORKSPACE,
+                            num_programs=tm * tn * s, **kw)
+    else:  # f32 C += A*B, then the steps
+        init = np.random.default_rng(case).uniform(-1, 1, (M, N)).astype(np.float32)
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_LOAD_C, mapping=mapping,
+                            split_k=1, reduction=tb.RED_NONE, num_programs=progs, **kw)
+    return cfg, init
+
+
+def test_random_fused_parity(device):
+    insts = [i for i in _every_instance() if i[7]]  # `_epi` instances
+    rng = random.Random(0x5EED0A00)
+    failures = []
+    for case in range(FUSED_CASES):
+        cfg, init = _fused_case(rng, insts, case)
+        desc = tb.GemmDesc.from_config(cfg)
+        print(f"fused case {case}: {cfg.m}x{cfg.n}x{cfg.k} {desc.kernel_name} mapping "
+              f"{cfg.mapping} programs {cfg.num_programs} split {cfg.split_k} bias "
+              f"{cfg.epi_bias} act {cfg.epi_activation} clamp {cfg.epi_clamp}", flush=True)
+        M, N, K = cfg.m, cfg.n, cfg.k
+        A, B = oracle.config_inputs(M, N, K, 0x5EED0A00 + case, oracle.NORMAL)
+        bias_host = None
+        bias_dev = None
+        if cfg.epi_bias:
+            v = oracle.fill_f16(1, N, 0x5EED0B00 + case, oracle.UNIFORM, 1.0).reshape(N)
+            host = v if cfg.epi_bias == tb.EPI_BIAS_F16 else v.astype(np.float32)
+            bias_dev = torch.from_numpy(np.ascontiguousarray(host)).to(device)
+            bias_host = host.astype(np.float64)
+        c_dtype = torch.float16 if cfg.c_dtype == tb.DTYPE_F16 else torch.float32
+        dA = torch.from_numpy(A).to(device)
+        dB = torch.from_numpy(B).to(device)
+        dC = (torch.full((M, N), float("nan"), dtype=c_dtype, device=device) if init is None
+              else torch.from_numpy(init.copy()).to(device))
+        ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=device)
+              if desc.workspace_bytes else None)
+        desc.launch(dA, dB, dC, ws, bias=bias_dev)
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(A, B, init=init)
+        oracle.epilogue_f64(ref, bias_host, cfg.epi_activation, cfg.epi_clamp,
+                            cfg.clamp_min, cfg.clamp_max)
+        bad, err, worst = oracle.check_tolerance(dC.cpu().numpy(), ref, rtol=RTOL)
+        if bad:
+            failures.append(f"fused case {case} ({desc.kernel_name}): {bad} violations, "
                             f"worst {err} at {worst}")
     assert not failures, "\n".join(failures)
