@@ -23,10 +23,12 @@
 
 // 256-wide macro-tiles (the MFMA-bound configs). 8 waves (2 per SIMD: one
 // wave's MFMAs run while the other waits) in the 4x2 grid the plan derives
-// for 8 waves on a 256x256 tile come first.
+// for 8 waves on a 256x256 tile come first. The 4x1 / 1x4 grids are the ones
+// the plan derives for 4 waves on 256x128 / 128x256 tiles.
 #define TBK_TILES_LARGE(X)                                                      \
   X(256, 256, 64, 4, 2, 2), X(256, 256, 32, 4, 2, 3), X(256, 256, 32, 4, 2, 4), \
       X(256, 256, 64, 2, 2, 2), X(256, 256, 32, 2, 2, 2),                       \
       X(256, 256, 32, 2, 2, 3), X(256, 256, 32, 2, 2, 4),                       \
       X(256, 128, 64, 2, 2, 2), X(256, 128, 64, 2, 2, 3),                       \
-      X(128, 256, 64, 2, 2, 2), X(128, 256, 64, 2, 2, 3)
+      X(128, 256, 64, 2, 2, 2), X(128, 256, 64, 2, 2, 3),                       \
+      X(256, 128, 64, 4, 1, 2), X(128, 256, 64, 1, 4, 2)

@@ -161,3 +161,50 @@ def test_random_fused_parity(device):
             failures.append(f"fused case {case} ({desc.kernel_name}): {bad} violations, "
                             f"worst {err} at {worst}")
     assert not failures, "\n".join(failures)
+
+
+PLAN_CASES = 150
+PLAN_TILES = [(64, 64, 32), (64, 64, 64), (128, 128, 32), (128, 128, 64), (128, 64, 64),
+              (64, 128, 64), (256, 256, 64), (256, 128, 64), (128, 256, 64)]
+
+
+def test_random_plan_pipeline_parity(device):
+    """Random tb.matmul modules through the plan pipeline (tile, waves,
+    stages, GROUP_M, split-K, persistent programs) and the C ABI, against
+    the oracle. Modules the plan refuses are skipped; most must run."""
+    from mini_triton_nvgpu_v1_amd import configs
+    rng = random.Random(0x5EED0C00)
+    ran, failures = 0, []
+    for case in range(PLAN_CASES):
+        bm, bn, bk = rng.choice(PLAN_TILES)
+        M, N, K = rng.randint(1, 700), 8 * rng.randint(1, 90), 8 * rng.randint(1, 160)
+        split = rng.choice([1, 1, 1, 2, 4, 8])
+        if split > -(-K // bk):  # the plan needs a k-tile per split
+            split = 1
+        persistent = split == 1 and rng.random() < 0.3
+        tiles = -(-M // bm) * -(-N // bn)
+        big = bm * bn >= 256 * 128  # 8 waves and 2 stages only for the large tiles
+        w = configs.Workload(
+            f"random_{case}", M, N, K, 0x5EED0C00 + case, rng.choice([0, 1]), (bm, bn, bk),
+            num_waves=rng.choice([4, 8]) if bm == bn == 256 else 4,
+            stages=2 if big else rng.choice([2, 3]), group_m=rng.choice([1, 4, 8]),
+            exact_tile=M % bm == 0 and N % bn == 0 and K % bk == 0, split_k=split,
+            persistent=persistent, num_ctas=rng.randint(1, tiles) if persistent else 1)
+        try:
+            desc = tb.plan_from_mlir(w.mlir())
+        except tb.TbError as e:
+            print(f"plan case {case}: {M}x{N}x{K} tile {(bm, bn, bk)} refused: {e}", flush=True)
+            continue
+        print(f"plan case {case}: {M}x{N}x{K} tile {(bm, bn, bk)} waves {w.num_waves} "
+              f"stages {w.stages} split {split} persistent {persistent} -> "
+              f"{desc.kernel_name}", flush=True)
+        A, B = oracle.config_inputs(M, N, K, w.seed, w.dist)
+        got = run_desc(desc, A, B, device)
+        ref = oracle.gemm_f64(A, B)
+        bad, err, worst = oracle.check_tolerance(got, ref, rtol=RTOL)
+        ran += 1
+        if bad:
+            failures.append(f"plan case {case} ({desc.kernel_name}): {bad} violations, "
+                            f"worst {err} at {worst}")
+    assert not failures, "\n".join(failures)
+    assert ran >= PLAN_CASES * 2 // 3, f"only {ran} of {PLAN_CASES} modules planned"
