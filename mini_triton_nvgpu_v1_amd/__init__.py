@@ -153,6 +153,35 @@ def _stream_handle(stream) -> int | None:
     return stream.cuda_stream  # torch.cuda.Stream -> hipStream_t
 
 
+def _is_tensor(x) -> bool:
+    return hasattr(x, "data_ptr") and hasattr(x, "untyped_storage")
+
+
+def _check_operand(x, role: str, dtypes: tuple, rows: int, cols: int, ld: int,
+                   elem: int) -> None:
+    """Check a torch tensor against what the kernels will touch through its
+    address: the element type, the row-major (rows x cols, leading dimension
+    ld) footprint inside the tensor's storage and the layout of a 2-D
+    tensor. Raw integer addresses are the caller's responsibility, as in the
+    C ABI."""
+    if x is None or not _is_tensor(x):
+        return
+    names = " or ".join(str(d).replace("torch.", "") for d in dtypes)
+    if x.dtype not in dtypes:
+        raise TbError(f"{role}: expected a {names} tensor, got {x.dtype}")
+    need = ((rows - 1) * ld + cols) * elem if rows > 0 and cols > 0 else 0
+    st = x.untyped_storage()
+    avail = st.data_ptr() + st.nbytes() - x.data_ptr()
+    if need > avail:
+        raise TbError(f"{role}: the descriptor touches {need} bytes from the tensor's "
+                      f"address, its storage holds {avail}")
+    if x.dim() == 2 and rows > 1 and cols > 1:
+        if x.shape[0] < rows or x.shape[1] < cols or x.stride(1) != 1 or x.stride(0) != ld:
+            raise TbError(f"{role}: a 2-D tensor must be at least {rows} x {cols}, "
+                          f"row-major with leading dimension {ld} (got shape "
+                          f"{tuple(x.shape)}, strides {tuple(x.stride())})")
+
+
 class GemmDesc:
     """Owning handle of a ``tb_gemm_desc``."""
 
@@ -189,26 +218,75 @@ class GemmDesc:
     def workspace_bytes(self) -> int:
         return lib().tb_workspace_bytes(self._h)
 
+    def check_operands(self, a, b, c, workspace=None, bias=None) -> None:
+        """Check torch tensors against this descriptor before their addresses
+        go to the C ABI: A (M x K, lda) and B (K x N, ldb) f16, C (M x N, ldc)
+        of the config's C type, the bias (N values of the bias type) and the
+        workspace (workspace_bytes). The kernels bound their accesses by the
+        descriptor's sizes, not the tensor's, so a short or mistyped tensor
+        would be written past its end. Raises TbError; raw integer addresses
+        pass unchecked."""
+        if not any(_is_tensor(x) for x in (a, b, c, workspace, bias)):
+            return
+        import torch
+        cf = self.config
+        f16, f32 = (torch.float16,), (torch.float32,)
+        _check_operand(a, "A", f16, cf.m, cf.k, cf.lda, 2)
+        _check_operand(b, "B", f16, cf.k, cf.n, cf.ldb, 2)
+        cdt, ce = (f16, 2) if cf.c_dtype == DTYPE_F16 else (f32, 4)
+        _check_operand(c, "C", cdt, cf.m, cf.n, cf.ldc, ce)
+        if cf.epi_bias != EPI_BIAS_NONE:
+            bdt, be = (f16, 2) if cf.epi_bias == EPI_BIAS_F16 else (f32, 4)
+            _check_operand(bias, "bias", bdt, 1, cf.n, cf.n, be)
+        if self.workspace_bytes and _is_tensor(workspace):
+            _check_operand(workspace, "workspace", (workspace.dtype,), 1,
+                           self.workspace_bytes, self.workspace_bytes, 1)
+        for role, x in (("A", a), ("B", b), ("C", c), ("workspace", workspace),
+                        ("bias", bias)):
+            if _is_tensor(x) and not x.is_cuda:
+                raise TbError(f"{role}: the tensor must be on a GPU (got {x.device})")
+        devs = {x.device for x in (a, b, c, workspace, bias) if _is_tensor(x)}
+        if len(devs) > 1:
+            raise TbError(f"operands are on different devices: {sorted(map(str, devs))}")
+
+    @staticmethod
+    def _default_stream(stream, *xs):
+        """An explicit stream wins; else torch's current stream of the
+        tensors' device (work queued there by torch then orders with the
+        GEMM); else the null stream."""
+        if stream is not None:
+            return _stream_handle(stream)
+        for x in xs:
+            if _is_tensor(x) and x.is_cuda:
+                import torch
+                return torch.cuda.current_stream(x.device).cuda_stream
+        return None
+
     def launch(self, a, b, c, workspace=None, stream=None, bias=None) -> None:
         """Enqueue C = A*B (or C += A*B), then the config's fused epilogue
         steps, for device tensors/addresses. ``bias`` (N values) is required
-        exactly when the config adds one."""
+        exactly when the config adds one. Tensors are checked against the
+        descriptor (check_operands); ``stream`` defaults to torch's current
+        stream of the tensors' device."""
+        self.check_operands(a, b, c, workspace, bias)
+        st = self._default_stream(stream, a, b, c)
         if bias is None:
             _check(lib().tb_gemm_launch(self._h, _ptr(a), _ptr(b), _ptr(c),
-                                        _ptr(workspace), _stream_handle(stream)))
+                                        _ptr(workspace), st))
         else:
             _check(lib().tb_gemm_launch_ex(self._h, _ptr(a), _ptr(b), _ptr(c),
-                                           _ptr(bias), _ptr(workspace),
-                                           _stream_handle(stream)))
+                                           _ptr(bias), _ptr(workspace), st))
 
     def bind(self, a, b, c, workspace=None, stream=None, bias=None):
         """A zero-argument launcher for repeated launches on the same buffers
-        and stream: device addresses and the stream handle are resolved once,
-        so each call is one C call (the shape of the reference's driver loop,
-        tools/bench_stage1_fair.py:680-699). The buffers must outlive it."""
+        and stream: the operands are checked, and device addresses and the
+        stream handle resolved, once, so each call is one C call (the shape of
+        the reference's driver loop, tools/bench_stage1_fair.py:680-699). The
+        buffers must outlive it."""
+        self.check_operands(a, b, c, workspace, bias)
         L = lib()
         args = (self._h, _ptr(a), _ptr(b), _ptr(c))
-        ws, st = _ptr(workspace), _stream_handle(stream)
+        ws, st = _ptr(workspace), self._default_stream(stream, a, b, c)
         if bias is None:
             fn, args = L.tb_gemm_launch, args + (ws, st)
         else:

@@ -404,7 +404,8 @@ def rocprof_case(case: FairCase, out_dir: Path, args) -> dict[str, Any]:
         return {"ok": False, "error": str(e)[:300]}
     (cdir / "rocprof.log").write_text(p.stdout + p.stderr)
     stats = sorted(cdir.rglob("*kernel_stats.csv"))
-    return {"ok": p.returncode in (0, 139) and bool(stats), "returncode": p.returncode,
+    # any nonzero exit is a failure, a crash of the profiled run included
+    return {"ok": p.returncode == 0 and bool(stats), "returncode": p.returncode,
             "kernel_stats": [str(s) for s in stats], "log": str(cdir / "rocprof.log")}
 
 

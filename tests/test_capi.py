@@ -179,3 +179,46 @@ def test_bound_launcher_checks_like_launch():
     plain = tb.GemmDesc.from_config(_cfg())
     with pytest.raises(tb.TbError, match="device pointers"):
         plain.bind(0, 16, 16)()
+
+
+def test_tensor_operands_checked_against_the_descriptor():
+    """GemmDesc.launch / bind check torch tensors before any GPU call: the
+    element type, the bytes the descriptor touches from the tensor's address,
+    a 2-D tensor's row-major layout, and the device (CPU tensors of the right
+    type and size get as far as the device check)."""
+    import torch
+    w = configs.SMOKE  # 64 x 64 x 32, f16 C
+    d = tb.GemmDesc.from_config(_cfg())
+    A = torch.zeros(w.M, w.K, dtype=torch.float16)
+    B = torch.zeros(w.K, w.N, dtype=torch.float16)
+    C = torch.zeros(w.M, w.N, dtype=torch.float16)
+    with pytest.raises(tb.TbError, match="C: expected a float16 tensor"):
+        d.launch(A, B, C.float())
+    with pytest.raises(tb.TbError, match="A: the descriptor touches 4096 bytes"):
+        d.launch(torch.zeros(w.M // 2, w.K, dtype=torch.float16), B, C)
+    with pytest.raises(tb.TbError, match="at least 64 x 32"):
+        d.launch(A[: w.M // 2], B, C)  # a view: storage enough, shape short
+    with pytest.raises(tb.TbError, match="B: expected a float16"):
+        d.bind(A, B.to(torch.bfloat16), C)
+    with pytest.raises(tb.TbError, match="row-major with leading dimension"):
+        d.launch(A, B, C.t())
+    with pytest.raises(tb.TbError, match="storage holds"):
+        d.launch(A, B, C[1:])
+    with pytest.raises(tb.TbError, match="must be on a GPU"):
+        d.launch(A, B, C)
+    # a flat buffer of enough bytes passes the size check
+    with pytest.raises(tb.TbError, match="must be on a GPU"):
+        d.launch(A, B, torch.zeros(w.M * w.N, dtype=torch.float16))
+    biased = tb.GemmDesc.from_config(_cfg(epi_bias=tb.EPI_BIAS_F32))
+    with pytest.raises(tb.TbError, match="bias: expected a float32"):
+        biased.launch(A, B, C, bias=torch.zeros(w.N, dtype=torch.float16))
+    with pytest.raises(tb.TbError, match="bias: the descriptor touches 256 bytes"):
+        biased.launch(A, B, C, bias=torch.zeros(w.N - 4, dtype=torch.float32))
+    sk = tb.GemmDesc.from_config(configs.SPLIT_K.direct_config())
+    s = configs.SPLIT_K
+    As = torch.zeros(s.M, s.K, dtype=torch.float16)
+    Bs = torch.zeros(s.K, s.N, dtype=torch.float16)
+    Cs = torch.zeros(s.M, s.N, dtype=torch.float16)
+    short = torch.zeros(sk.workspace_bytes // 4 - 1, dtype=torch.float32)
+    with pytest.raises(tb.TbError, match="workspace: the descriptor touches"):
+        sk.launch(As, Bs, Cs, short)

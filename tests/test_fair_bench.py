@@ -98,3 +98,26 @@ def test_short_run_writes_reports(tmp_path):
             assert c["other"] is None
     text = (out / "stage1_fair_report.txt").read_text()
     assert "===== 64x64x32 =====" in text and "mini_vs_hipblaslt=" in text
+
+
+@pytest.mark.parametrize("rc,ok", [(0, True), (139, False), (1, False)])
+def test_rocprof_capture_counts_any_nonzero_exit_as_failure(tmp_path, monkeypatch, rc, ok):
+    """A profiled run that crashes (139 = SIGSEGV) is a failed capture, even
+    when it left a kernel-stats file behind; the code and the log path are
+    recorded."""
+    import subprocess
+    import types
+
+    case = fb.select_cases("gemm_4096")[0]
+
+    def fake_run(cmd, **kw):
+        d = tmp_path / case.name / "rocprof"
+        (d / "x").mkdir(parents=True, exist_ok=True)
+        (d / "x" / "trace_kernel_stats.csv").write_text("Name,Calls\n")
+        return types.SimpleNamespace(returncode=rc, stdout="", stderr="")
+
+    monkeypatch.setattr(subprocess, "run", fake_run)
+    args = fb.parse_args(["--cases", case.name])
+    r = fb.rocprof_case(case, tmp_path, args)
+    assert r["ok"] is ok and r["returncode"] == rc
+    assert r["log"].endswith("rocprof.log")
