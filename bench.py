@@ -9,8 +9,13 @@ persistent workloads (`extra`), the live roofline of the dominant kernel and
 the host fp32 CPU baseline (the oracle's blocked OpenMP GEMM on this box's
 cores, on a bounded sample of the same workload).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra]
-       [--no-cpu] [--workload NAME]
+Timing: a clock-settle phase (--settle-s seconds of launches), W warm-up
+launches, then --rounds rounds of exactly K launches, each bracketed by a
+device synchronize; `value` and `ms_per_step` are the median round. The
+timed output is checked against torch.matmul in f32 on every 16th row.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--rounds R]
+       [--settle-s S] [--no-extra] [--no-cpu] [--workload NAME]
 """
 from __future__ import annotations
 
@@ -32,12 +37,20 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_workload(w, steps: int, warmup: int, device):
-    """Launch `w` steps times back to back; wall clock over the timed region
-    and HIP events on the launch stream around the whole timed region
-    (average launch duration = elapsed / steps; the GPU never idles in
-    between, so for kernels longer than the launch rate this is the kernel
-    duration, for tiny kernels it is the launch-rate-bound time per call)."""
+def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
+                  settle_s: float = 0.0):
+    """Time `w` through the plan pipeline's kernel.
+
+    Order: a clock-settle phase (launches back to back for `settle_s` seconds
+    of wall clock, so the timed rounds run at the part's sustained clock and
+    not on the ramp up from idle), `warmup` untimed launches, then `rounds`
+    rounds of exactly `steps` launches, each bracketed by a device
+    synchronize on both sides. Per round: the wall clock and HIP events
+    recorded on the launch stream around its launches (average launch
+    duration = elapsed / steps; the GPU never idles in between, so for
+    kernels longer than the launch rate this is the kernel duration). The
+    medians over rounds are reported (the reference's median-of-rounds
+    method, tools/bench_stage1_fair.py:702-716)."""
     import torch
     import mini_triton_nvgpu_v1_amd as tb
 
@@ -58,21 +71,57 @@ def time_workload(w, steps: int, warmup: int, device):
     tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
     tb.fill_seeded_f16(B, w.K, w.N, w.seed_b, w.dist, w.scale, stream=stream)
     launch = desc.bind(A, B, C, ws, stream=stream, bias=bias)
+    settle_launches = 0
+    if settle_s > 0:
+        t_end = time.perf_counter() + settle_s
+        while time.perf_counter() < t_end:
+            for _ in range(50):
+                launch()
+            settle_launches += 50
+            torch.cuda.synchronize(device)
     for _ in range(warmup):
         launch()
-    region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    torch.cuda.synchronize(device)
-    t0 = time.perf_counter()
-    region[0].record(stream)
-    for i in range(steps):
-        launch()
-    region[1].record(stream)
-    torch.cuda.synchronize(device)
-    wall = time.perf_counter() - t0
-    avg_ms = region[0].elapsed_time(region[1]) / steps
-    finite = bool(torch.isfinite(C).all().item())
-    return {"wall_s": wall, "avg_launch_ms": avg_ms, "kernel": desc.kernel_name,
-            "finite": finite}
+    walls, events = [], []
+    for _ in range(rounds):
+        region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        region[0].record(stream)
+        for _ in range(steps):
+            launch()
+        region[1].record(stream)
+        torch.cuda.synchronize(device)
+        walls.append(time.perf_counter() - t0)
+        events.append(region[0].elapsed_time(region[1]) / steps)
+    ok = verify_output(w, A, B, C, bias)
+    return {"wall_s": statistics.median(walls), "avg_launch_ms": statistics.median(events),
+            "round_wall_s": walls, "round_launch_ms": events, "kernel": desc.kernel_name,
+            "settle_launches": settle_launches, "verified": ok}
+
+
+def verify_output(w, A, B, C, bias):
+    """The timed launches' output against torch.matmul in f32 on the same
+    device buffers (an independent GEMM), with the fused steps applied, on
+    every 16th row: per-element |err| <= 1e-2 (|ref| + 1)."""
+    import torch
+
+    rows = torch.arange(0, w.M, 16, device=A.device)
+    ref = A[rows].float() @ B.float()
+    if bias is not None:
+        ref += bias.float().view(1, -1)
+    if w.activation == "relu":
+        ref = torch.relu(ref)
+    elif w.activation == "gelu_tanh":
+        ref = torch.nn.functional.gelu(ref, approximate="tanh")
+    elif w.activation == "silu":
+        ref = torch.nn.functional.silu(ref)
+    if w.clamp_min is not None or w.clamp_max is not None:
+        ref = torch.clamp(ref, w.clamp_min, w.clamp_max)
+    got = C[rows].float()
+    err = (got - ref).abs()
+    bad = int((~(err <= 1e-2 * (ref.abs() + 1))).sum().item())
+    return {"rows": int(rows.numel()), "violations": bad,
+            "max_abs_err": float(err.max().item()), "vs": "torch.matmul f32"}
 
 
 def plan_time_ms(w, reps: int = 20) -> float:
@@ -163,9 +212,13 @@ def load_traffic(workload: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # the timed region is ~40 ms; warm-up long enough for clocks to settle
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--rounds", type=int, default=5,
+                    help="timed rounds of --steps launches; medians are reported")
+    ap.add_argument("--settle-s", type=float, default=2.0,
+                    help="seconds of back-to-back launches before the warm-up, so the "
+                         "timed rounds see the sustained clock, not the ramp from idle")
     ap.add_argument("--workload", default="gemm_4096")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -181,17 +234,19 @@ def main() -> int:
 
     device = torch.device("cuda:0")
     w = configs.BY_NAME[args.workload]
-    log(f"bench: workload {w.name} {w.M}x{w.N}x{w.K} steps={args.steps} warmup={args.warmup}")
-    r = time_workload(w, args.steps, args.warmup, device)
-    if not r["finite"]:
-        log("bench: non-finite output")
+    log(f"bench: workload {w.name} {w.M}x{w.N}x{w.K} steps={args.steps} "
+        f"warmup={args.warmup} rounds={args.rounds} settle={args.settle_s}s")
+    r = time_workload(w, args.steps, args.warmup, device, args.rounds, args.settle_s)
+    if r["verified"]["violations"]:
+        log(f"bench: output check failed: {r['verified']}")
         return 1
     ms_per_step = r["wall_s"] * 1e3 / args.steps
     value = w.flop * args.steps / r["wall_s"] / 1e12
     avg_kernel_ms = r["avg_launch_ms"]
     achieved = w.flop / (avg_kernel_ms * 1e-3) / 1e12
     log(f"bench: {r['kernel']} wall {ms_per_step * 1e3:.1f} us/step, "
-        f"kernel avg {avg_kernel_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s")
+        f"kernel avg {avg_kernel_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s "
+        f"(rounds {[round(x * 1e3, 2) for x in r['round_launch_ms']]} us)")
 
     extra = {}
     if not args.no_extra:
@@ -200,7 +255,10 @@ def main() -> int:
                 continue
             # a few tens of ms of GPU time per extra: long enough for a steady clock
             steps = 200 if other.flop < 1e9 else (300 if other.flop < 2e11 else 60)
-            o = time_workload(other, steps, steps, device)
+            o = time_workload(other, steps, steps, device, rounds=5)
+            if o["verified"]["violations"]:
+                log(f"bench: {other.name} output check failed: {o['verified']}")
+                return 1
             us = o["avg_launch_ms"] * 1e3
             wall_us = o["wall_s"] * 1e6 / steps
             extra[other.name] = {
@@ -210,7 +268,7 @@ def main() -> int:
                 "frac_mfma_peak": round(other.flop / (us * 1e-6) / 1e12 / PEAK_TFLOPS_F16, 4),
                 "frac_hbm_peak": round(other.algo_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                 "plan_pipeline_ms": round(plan_time_ms(other), 3),
-                "kernel": o["kernel"], "finite": o["finite"]}
+                "kernel": o["kernel"], "verified_rows": o["verified"]["rows"]}
             log(f"bench: {other.name}: {extra[other.name]}")
 
     cpu = None
@@ -241,7 +299,16 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),
                      "peak": PEAK_TFLOPS_F16, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS_F16, 4),
-                     "traffic": load_traffic(w.name)},
+                     "traffic": load_traffic(w.name),
+                     "traffic_source": ("committed profile, not measured in this run: "
+                                        f"profiles/traffic_{w.name}.json (rocprofv3 --pmc "
+                                        "FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated)")},
+        "timing": {"rounds": args.rounds, "statistic": "median over rounds",
+                   "round_us_per_launch": [round(x * 1e3, 2) for x in r["round_launch_ms"]],
+                   "round_ms_per_step_wall": [round(x * 1e3 / args.steps, 5)
+                                              for x in r["round_wall_s"]],
+                   "settle_s": args.settle_s, "settle_launches": r["settle_launches"]},
+        "verified": r["verified"],
         "cpu_baseline": cpu,
         "extra": extra,
     }

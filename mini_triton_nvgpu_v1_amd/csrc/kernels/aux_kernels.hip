@@ -6,6 +6,7 @@
 //  * the seeded f16 input generator used by the benchmark harness.
 // Also aggregates the GEMM instance registry.
 #include "gemm_gfx950.h"
+#include "gemm_tiles.h"
 
 #include <math.h>
 
@@ -159,16 +160,18 @@ hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
 }
 
 // ---- instance registry ----------------------------------------------------
-const KernelEntry *entries_small(int *n);
-const KernelEntry *entries_mid(int *n);
-const KernelEntry *entries_large(int *n);
-const KernelEntry *entries_small_epi(int *n);
-const KernelEntry *entries_mid_epi(int *n);
-const KernelEntry *entries_large_epi(int *n);
+// One table per shape and flavour (gemm_inst.hip) plus the 16x16x32 tables.
+#define TBK_DECLARE(SHAPE)                                                      \
+  const KernelEntry *entries_##SHAPE(int *n);                                  \
+  const KernelEntry *entries_##SHAPE##_epi(int *n);
+TBK_SHAPES(TBK_DECLARE)
+#undef TBK_DECLARE
+const KernelEntry *entries_mfma16(int *n);
 
-static const KernelEntry *(*const kTables[])(int *) = {
-    entries_small,     entries_mid,     entries_large,
-    entries_small_epi, entries_mid_epi, entries_large_epi};
+#define TBK_TABLES(SHAPE) entries_##SHAPE, entries_##SHAPE##_epi,
+static const KernelEntry *(*const kTables[])(int *) = {TBK_SHAPES(TBK_TABLES)
+                                                           entries_mfma16};
+#undef TBK_TABLES
 
 int kernel_count() {
   int total = 0;

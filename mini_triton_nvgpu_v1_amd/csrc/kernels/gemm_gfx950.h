@@ -163,6 +163,21 @@ __device__ __forceinline__ void epi_dispatch(int act, int clamp, F &&f) {
   }
 }
 
+// The same with the clamp always applied as selects (bounds -inf / +inf for
+// a clamp that is off: the same comparisons, so the same results): four
+// variants of the unrolled code instead of eight, for the many general-loop
+// instances, whose build time this halves.
+template <typename F>
+__device__ __forceinline__ void epi_dispatch_act(int act, F &&f) {
+  using C1 = std::integral_constant<bool, true>;
+  switch (act) {
+  case 1: f(std::integral_constant<int, 1>{}, C1{}); break;
+  case 2: f(std::integral_constant<int, 2>{}, C1{}); break;
+  case 3: f(std::integral_constant<int, 3>{}, C1{}); break;
+  default: f(std::integral_constant<int, 0>{}, C1{}); break;
+  }
+}
+
 __device__ __forceinline__ float epi_apply1(float x, float bias, const EpiArgs &e) {
   x += bias;
   x = epi_activation(x, e.act);

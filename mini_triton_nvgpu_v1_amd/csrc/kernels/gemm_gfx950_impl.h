@@ -891,8 +891,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g)
           bv[j][g] = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
-      // the activation and clamp dispatched once (no branch per element);
-      // clamp bounds -inf / +inf for a clamp that is off
+      // the activation dispatched once (no branch per element); the clamps
+      // are selects against bounds that are -inf / +inf for a clamp that is off
       const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
       const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
       auto steps = [&](auto act_c, auto clamp_c) {
@@ -911,7 +911,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           __builtin_amdgcn_sched_barrier(0); // one 32-column tile at a time
         }
       };
-      epi_dispatch(p.epi_act, p.epi_clamp, steps);
+      epi_dispatch_act(p.epi_act, steps);
     }
 
     if constexpr (OUT == kOutF16 && T::STAGED_F16_EPILOGUE) {

@@ -1,0 +1,18 @@
+// The v_mfma_f32_16x16x32_f16 instances of the 4-wave 256x256x64 2-stage
+// f16 tile (whole tiles; tile, grouped or persistent order), plain and with
+// the fused epilogue steps.
+#include "gemm_gfx950_impl.h"
+
+namespace tbk {
+static const KernelEntry kMfma16[] = {
+    {{256, 256, 64, 2, 2, kOutF16, 2, 0, 1},
+     reinterpret_cast<const void *>(&gemm_mfma16<false>),
+     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"},
+    {{256, 256, 64, 2, 2, kOutF16, 2, 1, 1},
+     reinterpret_cast<const void *>(&gemm_mfma16<true>),
+     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi"}};
+const KernelEntry *entries_mfma16(int *n) {
+  *n = sizeof(kMfma16) / sizeof(kMfma16[0]);
+  return kMfma16;
+}
+} // namespace tbk

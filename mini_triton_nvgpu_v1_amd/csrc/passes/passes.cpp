@@ -3,6 +3,7 @@
 // from tb-opt), derives its plan and writes it as an attribute, exactly as
 // the reference passes do (lib/Transforms/*.cpp).
 #include "passes.h"
+#include "../plan/instances.h"
 
 #include "../plan/contract.h"
 #include "../plan/plans.h"
@@ -668,26 +669,10 @@ tb_gemm_config launchConfigOf(const Op &launch) {
   return g;
 }
 
-// Mirrors the runtime's instance selection (output mode from C type, C
-// init and reduction) so tb-opt can name the kernel without a GPU.
+// The instance the runtime binds (instances.h), so tb-opt can name the
+// kernel without a GPU.
 std::string kernelInstanceName(const tb_gemm_config &c) {
-  int out;
-  if (c.mapping == TB_MAP_SPLIT_K)
-    out = c.reduction == TB_RED_ATOMIC ? 3 : 1;
-  else if (c.c_dtype == TB_DTYPE_F16)
-    out = 0;
-  else
-    out = c.acc_init == TB_ACC_INIT_LOAD_C ? 2 : 1;
-  // fused epilogue steps run in an `_epi` instance, except on split-K
-  // partials (the reduction applies them)
-  const bool epi = (c.epi_bias || c.epi_activation || c.epi_clamp) &&
-                   c.mapping != TB_MAP_SPLIT_K;
-  char buf[128];
-  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d%s%s",
-           (long long)c.block_m, (long long)c.block_n, (long long)c.block_k,
-           (long long)c.wave_grid_m, (long long)c.wave_grid_n, (long long)c.stages,
-           out, c.mfma == TB_MFMA_16X16X32 ? "_16x16x32" : "", epi ? "_epi" : "");
-  return buf;
+  return instanceName(instanceKeyOf(c));
 }
 
 } // namespace tb

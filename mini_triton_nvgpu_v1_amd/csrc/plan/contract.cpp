@@ -1,6 +1,7 @@
 // KernelContract: the public plan attributes of a sealed tb.pipeline_mainline,
 // its verifier, and its flattening into the gfx950 launch configuration.
 #include "contract.h"
+#include "instances.h"
 #include "serialize.h"
 
 #include <algorithm>
@@ -245,6 +246,11 @@ tb_gemm_config lowerContractToConfig(const KernelContract &k) {
   g.mfma = c.mmaKind == MmaKind::Mfma16x16x32F16 ? TB_MFMA_16X16X32 : TB_MFMA_32X32X16;
   if (g.mfma == TB_MFMA_16X16X32 && g.mapping == TB_MAP_SPLIT_K)
     throw Error("mma = `mfma_f32_16x16x32_f16` has no split-k instance");
+  // the lowering names only kernels that exist
+  const InstanceKey key = instanceKeyOf(g);
+  if (!hasGfx950Instance(key))
+    throw Error("no gfx950 kernel instance `" + instanceName(key) +
+                "` for this contract (see tb-opt --list-instances)");
   return g;
 }
 

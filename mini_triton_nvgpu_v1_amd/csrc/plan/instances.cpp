@@ -1,0 +1,94 @@
+// Host-side table of the compiled gfx950 kernel instances (see instances.h).
+#include "instances.h"
+
+#include "../kernels/gemm_tiles.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <set>
+#include <tuple>
+
+namespace tb {
+
+static auto tie(const InstanceKey &k) {
+  return std::tie(k.bm, k.bn, k.bk, k.wgm, k.wgn, k.out, k.stages, k.epi, k.mfma);
+}
+bool InstanceKey::operator<(const InstanceKey &o) const { return tie(*this) < tie(o); }
+bool InstanceKey::operator==(const InstanceKey &o) const { return tie(*this) == tie(o); }
+
+namespace {
+struct Tile {
+  int64_t bm, bn, bk, wgm, wgn, stages;
+};
+#define TB_TILE(BM, BN, BK, WGM, WGN, ST) Tile{BM, BN, BK, WGM, WGN, ST}
+#define TB_SHAPE_TILES(SHAPE) TBK_TILES_##SHAPE(TB_TILE),
+const Tile kTiles[] = {TBK_SHAPES(TB_SHAPE_TILES)};
+#undef TB_SHAPE_TILES
+#undef TB_TILE
+} // namespace
+
+const std::vector<InstanceKey> &gfx950Instances() {
+  static const std::vector<InstanceKey> all = [] {
+    std::vector<InstanceKey> v;
+    for (const Tile &t : kTiles) {
+      for (int out = kInstOutF16; out <= kInstOutF32Atomic; ++out)
+        v.push_back({t.bm, t.bn, t.bk, t.wgm, t.wgn, out, t.stages, 0, TB_MFMA_32X32X16});
+      // the fused steps need the whole sum: no atomic-output flavour
+      for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
+        v.push_back({t.bm, t.bn, t.bk, t.wgm, t.wgn, out, t.stages, 1, TB_MFMA_32X32X16});
+    }
+    for (int epi = 0; epi <= 1; ++epi)
+      v.push_back({256, 256, 64, 2, 2, kInstOutF16, 2, epi, TB_MFMA_16X16X32});
+    return v;
+  }();
+  return all;
+}
+
+bool hasGfx950Instance(const InstanceKey &k) {
+  static const std::set<InstanceKey> keys(gfx950Instances().begin(),
+                                          gfx950Instances().end());
+  return keys.count(k) != 0;
+}
+
+std::string instanceName(const InstanceKey &k) {
+  char buf[128];
+  snprintf(buf, sizeof buf, "tb_gemm_gfx950_%lldx%lldx%lld_w%lldx%lld_s%lld_out%d%s%s",
+           (long long)k.bm, (long long)k.bn, (long long)k.bk, (long long)k.wgm,
+           (long long)k.wgn, (long long)k.stages, k.out,
+           k.mfma == TB_MFMA_16X16X32 ? "_16x16x32" : "", k.epi ? "_epi" : "");
+  return buf;
+}
+
+InstanceKey instanceKeyOf(const tb_gemm_config &c) {
+  InstanceKey k;
+  k.bm = c.block_m;
+  k.bn = c.block_n;
+  k.bk = c.block_k;
+  k.wgm = c.wave_grid_m;
+  k.wgn = c.wave_grid_n;
+  k.stages = c.stages;
+  if (c.mapping == TB_MAP_SPLIT_K)
+    k.out = c.reduction == TB_RED_ATOMIC ? kInstOutF32Atomic : kInstOutF32Partial;
+  else if (c.c_dtype == TB_DTYPE_F16)
+    k.out = kInstOutF16;
+  else
+    k.out = c.acc_init == TB_ACC_INIT_LOAD_C ? kInstOutF32Accum : kInstOutF32Partial;
+  k.epi = (c.epi_bias || c.epi_activation || c.epi_clamp) && c.mapping != TB_MAP_SPLIT_K;
+  k.mfma = c.mfma;
+  return k;
+}
+
+std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>
+compiledWaveGrids(int64_t bm, int64_t bn, int64_t bk) {
+  std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>> v;
+  for (const Tile &t : kTiles)
+    if (t.bm == bm && t.bn == bn && t.bk == bk)
+      v.push_back({{t.wgm, t.wgn}, t.stages});
+  std::sort(v.begin(), v.end(), [](const auto &a, const auto &b) {
+    return std::make_tuple(a.first.first * a.first.second, a.first.first, a.second) <
+           std::make_tuple(b.first.first * b.first.second, b.first.first, b.second);
+  });
+  return v;
+}
+
+} // namespace tb

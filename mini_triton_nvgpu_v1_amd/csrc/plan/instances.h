@@ -1,0 +1,49 @@
+// The gfx950 kernel instances compiled into libtb_gfx950.so, as host data:
+// the tile lists of kernels/gemm_tiles.h in every output mode (plain) and in
+// the whole-result modes (fused epilogue steps), plus the 16x16x32
+// instances. KernelConfig legality and tb-lower-pipeline-to-gfx950 consult
+// this table, so the plan refuses a configuration with no kernel and the
+// lowering never names one that does not exist. tb-opt carries it without
+// the kernels (`tb-opt --list-instances`).
+#pragma once
+
+#include "tb_gfx950.h"
+
+#include <cstdint>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace tb {
+
+// Output modes of an instance (the kernels' OutMode).
+enum InstanceOut : int {
+  kInstOutF16 = 0,        // C(f16) = A*B
+  kInstOutF32Partial = 1, // f32 store: split-K partial plane, or plain f32 C
+  kInstOutF32Accum = 2,   // C(f32) += A*B
+  kInstOutF32Atomic = 3,  // C(f32) += partial sums with atomics
+};
+
+struct InstanceKey {
+  int64_t bm = 0, bn = 0, bk = 0, wgm = 0, wgn = 0;
+  int out = 0;
+  int64_t stages = 0;
+  int epi = 0;  // 1: the fused epilogue steps are compiled in
+  int mfma = 0; // TB_MFMA_*
+  bool operator<(const InstanceKey &o) const;
+  bool operator==(const InstanceKey &o) const;
+};
+
+const std::vector<InstanceKey> &gfx950Instances();
+bool hasGfx950Instance(const InstanceKey &k);
+// tb_gemm_gfx950_{BM}x{BN}x{BK}_w{WGM}x{WGN}_s{S}_out{OUT}[_16x16x32][_epi]
+std::string instanceName(const InstanceKey &k);
+// The instance a flattened configuration binds: the output mode follows
+// from C's type, C's initialisation and the reduction; split-K partials take
+// the fused steps in the reduction, so they bind the plain instance.
+InstanceKey instanceKeyOf(const tb_gemm_config &c);
+// (wave grid, stages) pairs compiled for a block shape on 32x32x16 MFMA.
+std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>
+compiledWaveGrids(int64_t bm, int64_t bn, int64_t bk);
+
+} // namespace tb

@@ -51,8 +51,8 @@ template <class V> void fields(V &v, EncodingPlan &p) {
 // over wave grids whose wave tiles are whole MFMA tiles; ties go to more
 // waves along the longer block side (M for a square block, which the
 // reference's two_warp_shape_closure_contract test pins).
-static std::pair<int64_t, int64_t> deriveWaveGrid(const KernelConfig &c,
-                                                  int64_t instrM, int64_t instrN) {
+std::pair<int64_t, int64_t> deriveWaveGrid(const KernelConfig &c, int64_t instrM,
+                                           int64_t instrN) {
   int64_t bestM = -1, bestN = -1, bestScore = std::numeric_limits<int64_t>::max();
   for (int64_t gm = 1; gm <= c.numWarps; ++gm) {
     if (c.numWarps % gm)

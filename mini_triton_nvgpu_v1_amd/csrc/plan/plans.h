@@ -90,6 +90,11 @@ const char *mmaKindName(MmaKind k);
 int64_t scalarBytes(ScalarKind k);
 KernelConfig getKernelConfig(const Module &m, const Op &matmul);
 void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t);
+// The wave grid the EncodingPlan derives (reference EncodingPlan.cpp:283-320):
+// minimal |wave_tile_m - wave_tile_n| over grids of whole instrM x instrN
+// tiles, ties to more waves along the longer block side.
+std::pair<int64_t, int64_t> deriveWaveGrid(const KernelConfig &c, int64_t instrM,
+                                           int64_t instrN);
 
 // ---- MatmulSemantics (reference MatmulSemantics.h:15-31) ------------------
 struct MatmulSemantics {

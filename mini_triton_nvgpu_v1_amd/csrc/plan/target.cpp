@@ -1,5 +1,6 @@
 // TargetInfo (gfx950 capability table), KernelConfig legality and
 // MatmulSemantics.
+#include "instances.h"
 #include "serialize.h"
 
 #include <cstdlib>
@@ -230,6 +231,37 @@ KernelConfig getKernelConfig(const Module &m, const Op &op) {
   return k;
 }
 
+// The gfx950 kernels are compiled instances (kernels/gemm_tiles.h): a
+// 32x32x16 configuration is legal only where the wave grid the encoding plan
+// will derive has an instance for this block shape and stage count. (The
+// reference emits a kernel for any legal contract, LowerPipelineToNVGPU.cpp:
+// 678-1554; here the legality stops what the lowering could not bind.) A
+// configuration with no legal wave grid at all is left to the encoding
+// plan's own diagnostic.
+static void verifyCompiledInstance(const KernelConfig &c) {
+  if (c.mmaKind != MmaKind::Mfma32x32x16F16)
+    return; // 16x16x32: mfma16x16x32Supported above
+  std::pair<int64_t, int64_t> g;
+  try {
+    g = deriveWaveGrid(c, 32, 32);
+  } catch (const Error &) {
+    return;
+  }
+  for (const auto &[grid, stages] : compiledWaveGrids(c.blockM, c.blockN, c.blockK))
+    if (grid == g && stages == c.requestedStages)
+      return;
+  std::string have;
+  for (const auto &[grid, stages] : compiledWaveGrids(c.blockM, c.blockN, c.blockK))
+    have += (have.empty() ? "" : ", ") + std::to_string(grid.first) + "x" +
+            std::to_string(grid.second) + " s" + std::to_string(stages);
+  throw Error("no gfx950 kernel instance for block " + std::to_string(c.blockM) + "x" +
+              std::to_string(c.blockN) + "x" + std::to_string(c.blockK) + " on " +
+              std::to_string(c.numWarps) + " waves (wave grid " +
+              std::to_string(g.first) + "x" + std::to_string(g.second) + ") with " +
+              std::to_string(c.requestedStages) + " LDS stages; compiled wave grids " +
+              "and stages for this block: " + (have.empty() ? "none" : have));
+}
+
 // Reference: KernelConfig.cpp:202-246. gfx950 legality: f16 x f16 into an
 // f16 or f32 C through v_mfma_f32_32x32x16_f16, so the block shape must be
 // a multiple of the MFMA tile (32 x 32, k 16) and block_k one or two
@@ -272,6 +304,8 @@ void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t) {
   if (t && lds > t->maxSharedBytesPerCTA)
     throw Error("A/B stage buffers (" + std::to_string(lds) +
                 " bytes) exceed the target LDS budget");
+  if (t) // with the gfx950 target attached: its compiled kernels
+    verifyCompiledInstance(c);
 }
 
 // ---- MatmulSemantics -------------------------------------------------------------

@@ -8,6 +8,7 @@
 //
 // Diagnostics go to stderr as `<file>: error: <message>` with exit code 1.
 #include "../passes/passes.h"
+#include "../plan/instances.h"
 
 #include <cstdio>
 #include <cstring>
@@ -34,7 +35,8 @@ std::string readAll(const std::string &path) {
 void usage() {
   std::printf("usage: tb-opt [input.mlir|-] [-o output] "
               "[--pass-pipeline='builtin.module(...)'] [--<pass>[=<options>]]...\n"
-              "       tb-opt --list-passes\n");
+              "       tb-opt --list-passes\n"
+              "       tb-opt --list-instances   (the gfx950 kernels a plan can bind)\n");
 }
 
 } // namespace
@@ -52,6 +54,11 @@ int main(int argc, char **argv) {
       if (a == "--list-passes") {
         for (const tb::PassInfo &p : tb::registeredPasses())
           std::printf("%-40s %s\n", p.name.c_str(), p.summary.c_str());
+        return 0;
+      }
+      if (a == "--list-instances") {
+        for (const tb::InstanceKey &k : tb::gfx950Instances())
+          std::printf("%s\n", tb::instanceName(k).c_str());
         return 0;
       }
       if (a == "-o") {

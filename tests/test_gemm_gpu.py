@@ -6,6 +6,9 @@ per element with |got - ref| <= 1e-2 * (|ref| + 1) (f16 A/B, f32
 accumulation, the tolerance BASELINE.json states). Outputs are pre-filled
 with NaN so an element the kernel fails to write fails the check.
 """
+import dataclasses
+import time
+
 import numpy as np
 import pytest
 import torch
@@ -61,15 +64,52 @@ def test_workload_parity(w, device):
     check(got, A, B)
 
 
-def test_persistent_8192_parity_row_sample(device):
-    """8192^3: fp64 on sampled row blocks (first, a tile seam, last)."""
+@pytest.fixture(scope="module")
+def persistent_8192_ref():
+    """The 8192^3 workload's seeded inputs and the whole fp64 product (all
+    8192 rows; the OpenMP oracle takes tens of seconds on the box's cores)."""
+    w = configs.PERSISTENT
+    A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
+    t0 = time.perf_counter()
+    ref = oracle.gemm_f64(A, B)
+    print(f"fp64 oracle 8192^3: {time.perf_counter() - t0:.1f} s", flush=True)
+    return A, B, ref
+
+
+def _check_full(got, ref):
+    bad, err, worst = oracle.check_tolerance(got, ref, rtol=RTOL)
+    print(f"all {ref.shape[0]} rows: violations={bad} max|err|={err:.3e} at {worst}",
+          flush=True)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
+
+
+def test_persistent_8192_parity(device, persistent_8192_ref):
+    """8192^3 through the plan (256x256 tiles, 256 resident programs striding
+    over 1024 tiles in grouped order): every element against fp64."""
     w = configs.PERSISTENT
     print(f"workload {w.name}", flush=True)
-    A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
+    A, B, ref = persistent_8192_ref
     desc = tb.plan_from_mlir(w.mlir())
-    got = run_desc(desc, A, B, device)
-    assert not np.isnan(got).any()
-    check(got, A, B, rows=[(0, 40), (4080, 4128), (8150, 8192)])
+    assert desc.config.num_programs == 256
+    _check_full(run_desc(desc, A, B, device), ref)
+
+
+def test_persistent_8192_192x128_tiles(device, persistent_8192_ref):
+    """The persistent configuration on 192x128 tiles (the reference's
+    smoke_persistent_192x128x32 shape family, scaled): 43 x 64 tiles whose
+    last tile row is ragged (8192 = 42 * 192 + 128), 256 resident programs in
+    grouped order, so the ragged persistent edge runs at scale. Every
+    element against fp64."""
+    w = dataclasses.replace(configs.PERSISTENT, name="persistent_8192_192x128",
+                            block=(192, 128, 64), exact_tile=False)
+    print(f"workload {w.name}", flush=True)
+    A, B, ref = persistent_8192_ref
+    desc = tb.plan_from_mlir(w.mlir())
+    cfg = desc.config
+    assert (cfg.block_m, cfg.block_n, cfg.num_programs) == (192, 128, 256)
+    assert cfg.mapping == tb.MAP_PERSISTENT_GROUPED
+    print(f"kernel {desc.kernel_name}", flush=True)
+    _check_full(run_desc(desc, A, B, device), ref)
 
 
 # The configurations of the reference's examples/*.mlir and contract tests

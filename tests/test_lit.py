@@ -3,7 +3,8 @@
 Each file carries `// RUN:` lines in the reference's lit style
 (test/Transforms/*.mlir, run there by lit.cfg.py with %tb-opt substituted);
 this runner substitutes %tb-opt, %s and FileCheck and runs the line under
-bash -o pipefail. The CHECK lines are the gfx950 contract: where the
+bash -o pipefail, with lit's `not` (succeeds when its command fails) as a
+shell function. The CHECK lines are the gfx950 contract: where the
 reference checks a target-independent fact (mapping kinds, reduction kinds,
 wave grids, persistent residency) the check is the same; where it checks an
 NVIDIA-specific choice (LDS swizzle, epilogue reorder, NVGPU lowering) the
@@ -50,6 +51,7 @@ def test_lit(path):
     for cmd in runs:
         cmd = (cmd.replace("%tb-opt", str(TB_OPT)).replace("%s", str(path))
                .replace("FileCheck", str(FILECHECK)))
+        cmd = 'not() { if "$@"; then return 1; else return 0; fi; }; ' + cmd
         proc = subprocess.run(["bash", "-o", "pipefail", "-c", cmd],
                               capture_output=True, text=True, timeout=120,
                               env=dict(os.environ))

@@ -241,3 +241,52 @@ def test_cleanup_layout_conversions():
     out = tb_opt(text, "--tb-cleanup-layout-conversions").stdout
     assert "tb.convert_layout" not in out
     assert "tb.matmul %A, %B, %C" in out
+
+
+def test_tb_opt_instance_table_equals_the_kernel_registry():
+    """tb-opt carries the instance table without the kernels; it lists
+    exactly the instances compiled into libtb_gfx950.so, by the same names."""
+    p = subprocess.run([str(TB_OPT), "--list-instances"], capture_output=True,
+                       text=True, timeout=60, check=True)
+    listed = p.stdout.split()
+    assert len(listed) == len(set(listed))
+    assert sorted(listed) == sorted(tb.kernel_names())
+
+
+# every block shape with an instance list, 1 to 8 waves, 2 to 4 stages,
+# block_k 32 and 64, f16 and f32 C, plus shapes with no list at all
+SWEEP_BLOCKS = [(64, 64), (64, 128), (128, 64), (128, 128), (64, 256), (256, 64),
+                (128, 256), (256, 128), (256, 256), (192, 128), (96, 64), (160, 96)]
+
+
+@pytest.mark.parametrize("bm,bn", SWEEP_BLOCKS, ids=lambda v: str(v))
+def test_no_plan_legal_configuration_lacks_a_kernel(bm, bn):
+    """The plan either refuses a configuration (with a diagnostic) or binds
+    it to a compiled kernel: nothing that passes the plan pipeline and its
+    lowering fails at tb_desc_create for want of an instance. The lowering
+    names exactly the instance the runtime binds."""
+    bound = 0
+    for bk in (32, 64):
+        for warps in (1, 2, 4, 8):
+            for stages in (2, 3, 4):
+                for c in ("f16", "f32"):
+                    M = N = 768 if max(bm, bn) <= 256 else 1536
+                    text = matmul_module(M=M, N=N, K=256, bm=bm, bn=bn, bk=bk,
+                                         warps=warps, stages=stages, c=c,
+                                         exact=M % bm == 0 and N % bn == 0)
+                    try:
+                        d = tb.plan_from_mlir(text)
+                    except tb.TbError as e:
+                        msg = str(e)
+                        # a plan refusal names the pass; the runtime's own
+                        # "no gfx950 kernel instance for tile" must not occur
+                        assert re.match(r"tb_plan_from_mlir: tb-[a-z0-9-]+: ", msg), msg
+                        continue
+                    bound += 1
+                    cfg = d.config
+                    grid = configs.wave_grid(bm, bn, warps)
+                    assert (cfg.wave_grid_m, cfg.wave_grid_n) == grid
+                    assert d.kernel_name.startswith(
+                        f"tb_gemm_gfx950_{bm}x{bn}x{bk}_w{grid[0]}x{grid[1]}_s{stages}_")
+    if (bm, bn) not in ((96, 64), (160, 96)):
+        assert bound > 0

@@ -11,6 +11,7 @@ workspace, 2 .. 6 atomic). The seed is fixed, so a failure reproduces; its
 case line is printed before the launch.
 """
 import random
+import re
 
 import numpy as np
 import pytest
@@ -163,15 +164,19 @@ def test_random_fused_parity(device):
     assert not failures, "\n".join(failures)
 
 
-PLAN_CASES = 150
-PLAN_TILES = [(64, 64, 32), (64, 64, 64), (128, 128, 32), (128, 128, 64), (128, 64, 64),
-              (64, 128, 64), (256, 256, 64), (256, 128, 64), (128, 256, 64)]
+PLAN_CASES = 200
+PLAN_TILES = [(64, 64, 32), (64, 64, 64), (128, 128, 32), (128, 128, 64), (128, 64, 32),
+              (128, 64, 64), (64, 128, 32), (64, 128, 64), (256, 256, 32), (256, 256, 64),
+              (256, 128, 32), (256, 128, 64), (128, 256, 32), (128, 256, 64),
+              (64, 256, 64), (256, 64, 32), (192, 128, 64)]
 
 
 def test_random_plan_pipeline_parity(device):
-    """Random tb.matmul modules through the plan pipeline (tile, waves,
-    stages, GROUP_M, split-K, persistent programs) and the C ABI, against
-    the oracle. Modules the plan refuses are skipped; most must run."""
+    """Random tb.matmul modules through the plan pipeline (tile, 1-8 waves,
+    2-4 stages, GROUP_M, split-K, persistent programs) and the C ABI, against
+    the oracle. A module may be refused by a plan pass (a legality rule, the
+    LDS or register budget, or a wave grid with no compiled kernel); one the
+    plan accepts must bind a kernel and match."""
     from mini_triton_nvgpu_v1_amd import configs
     rng = random.Random(0x5EED0C00)
     ran, failures = 0, []
@@ -183,17 +188,21 @@ def test_random_plan_pipeline_parity(device):
             split = 1
         persistent = split == 1 and rng.random() < 0.3
         tiles = -(-M // bm) * -(-N // bn)
-        big = bm * bn >= 256 * 128  # 8 waves and 2 stages only for the large tiles
         w = configs.Workload(
             f"random_{case}", M, N, K, 0x5EED0C00 + case, rng.choice([0, 1]), (bm, bn, bk),
-            num_waves=rng.choice([4, 8]) if bm == bn == 256 else 4,
-            stages=2 if big else rng.choice([2, 3]), group_m=rng.choice([1, 4, 8]),
+            num_waves=rng.choice([1, 2, 4, 4, 8, 8]), stages=rng.choice([2, 3, 4]),
+            group_m=rng.choice([1, 4, 8]),
             exact_tile=M % bm == 0 and N % bn == 0 and K % bk == 0, split_k=split,
             persistent=persistent, num_ctas=rng.randint(1, tiles) if persistent else 1)
         try:
             desc = tb.plan_from_mlir(w.mlir())
         except tb.TbError as e:
-            print(f"plan case {case}: {M}x{N}x{K} tile {(bm, bn, bk)} refused: {e}", flush=True)
+            # only a plan pass may refuse (its name leads the message); the
+            # runtime's "no gfx950 kernel instance for tile" would mean the
+            # plan accepted a configuration with no kernel
+            assert re.match(r"tb_plan_from_mlir: tb-[a-z0-9-]+: ", str(e)), str(e)
+            print(f"plan case {case}: {M}x{N}x{K} tile {(bm, bn, bk)} waves "
+                  f"{w.num_waves} stages {w.stages} refused: {e}", flush=True)
             continue
         print(f"plan case {case}: {M}x{N}x{K} tile {(bm, bn, bk)} waves {w.num_waves} "
               f"stages {w.stages} split {split} persistent {persistent} -> "
@@ -207,4 +216,4 @@ def test_random_plan_pipeline_parity(device):
             failures.append(f"plan case {case} ({desc.kernel_name}): {bad} violations, "
                             f"worst {err} at {worst}")
     assert not failures, "\n".join(failures)
-    assert ran >= PLAN_CASES * 2 // 3, f"only {ran} of {PLAN_CASES} modules planned"
+    assert ran >= PLAN_CASES // 2, f"only {ran} of {PLAN_CASES} modules planned"
