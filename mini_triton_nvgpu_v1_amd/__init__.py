@@ -94,6 +94,15 @@ def lib() -> ctypes.CDLL:
         raise TbError(
             f"{LIB_PATH} is missing: build the gfx950 backend first "
             "(make -C mini_triton_nvgpu_v1_amd, or __graft_entry__.build())")
+    # PyTorch-ROCm ships its own HIP runtime (torch/lib/libamdhip64.so, with
+    # its own HSA runtime). Loaded first, torch's copy is the one this
+    # library binds (same soname); loaded after this library had pulled in
+    # /opt/rocm's, torch would load its copy as well, and two runtimes in one
+    # process do not share the GPU (hipLaunchKernel: "no ROCm-capable
+    # device"). So torch, when installed, is imported before the library.
+    import importlib.util
+    if importlib.util.find_spec("torch") is not None:
+        import torch  # noqa: F401
     L = ctypes.CDLL(LIB_PATH)
     vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
     pdesc = ctypes.POINTER(vp)
