@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define TB_GFX950_ABI_VERSION 3
+#define TB_GFX950_ABI_VERSION 4
 
 /* element types (reference ScalarKind, include/tb/Analysis/KernelConfig.h:13-16) */
 #define TB_DTYPE_F16 0
@@ -168,6 +168,25 @@ int tb_gemm_launch(const tb_gemm_desc *desc, const void *a, const void *b,
  * tb.matmul never takes. */
 int tb_gemm_launch_ex(const tb_gemm_desc *desc, const void *a, const void *b,
                       void *c, const void *bias, void *workspace, void *stream);
+
+/* Bytes of the static split-K scratch tb_gemm_launch_noalloc uses on each
+ * GPU (32 MiB: 8 splits of a 1024 x 1024 f32 result). */
+#define TB_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+
+/* tb_gemm_launch_ex without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): a split-K descriptor's f32 partials go to
+ * a static scratch array of TB_NOALLOC_SCRATCH_BYTES in the library, one per
+ * GPU, held until the process ends. It calls no hipMalloc, hipFree or other
+ * allocating routine, and fails with a clear error when the descriptor needs
+ * more workspace than the scratch holds (tb_workspace_bytes). Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU (other
+ * streams, other threads) race. Nothing in the scratch needs clearing: each
+ * call writes every partial its reduction reads. No counterpart in the
+ * reference, whose kernels keep their scratch in static shared memory
+ * (LowerPipelineToNVGPU.cpp:2701-2712) and have no global workspace. */
+int tb_gemm_launch_noalloc(const tb_gemm_desc *desc, const void *a, const void *b,
+                           void *c, const void *bias, void *stream);
 
 void tb_desc_free(tb_gemm_desc *desc);
 

@@ -24,7 +24,7 @@ __all__ = [
     "MAP_PERSISTENT_GROUPED", "RED_NONE", "RED_WORKSPACE", "RED_ATOMIC",
     "EPI_BIAS_NONE", "EPI_BIAS_F16", "EPI_BIAS_F32", "ACT_NONE", "ACT_RELU",
     "ACT_GELU_TANH", "ACT_SILU", "CLAMP_MIN", "CLAMP_MAX", "MFMA_32X32X16",
-    "MFMA_16X16X32",
+    "MFMA_16X16X32", "NOALLOC_SCRATCH_BYTES",
 ]
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -42,6 +42,8 @@ ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_SILU = 0, 1, 2, 3
 CLAMP_MIN, CLAMP_MAX = 1, 2
 # MFMA instruction of the instance (the EncodingPlan's instrShape)
 MFMA_32X32X16, MFMA_16X16X32 = 0, 1
+# static split-K scratch of tb_gemm_launch_noalloc per GPU
+NOALLOC_SCRATCH_BYTES = 32 * 1024 * 1024
 
 
 class TbError(RuntimeError):
@@ -128,6 +130,8 @@ def lib() -> ctypes.CDLL:
     L.tb_gemm_launch.restype = ctypes.c_int
     L.tb_gemm_launch_ex.argtypes = [vp, vp, vp, vp, vp, vp, vp]
     L.tb_gemm_launch_ex.restype = ctypes.c_int
+    L.tb_gemm_launch_noalloc.argtypes = [vp, vp, vp, vp, vp, vp]
+    L.tb_gemm_launch_noalloc.restype = ctypes.c_int
     L.tb_desc_free.argtypes = [vp]
     L.tb_desc_free.restype = None
     L.tb_fill_seeded_f16.argtypes = [vp, i64, i64, i64, ctypes.c_uint64, i32,
@@ -285,6 +289,16 @@ class GemmDesc:
         else:
             _check(lib().tb_gemm_launch_ex(self._h, _ptr(a), _ptr(b), _ptr(c),
                                            _ptr(bias), _ptr(workspace), st))
+
+    def launch_noalloc(self, a, b, c, stream=None, bias=None) -> None:
+        """Like launch, with no workspace argument: a split-K descriptor's
+        partials go to the library's static per-GPU scratch
+        (NOALLOC_SCRATCH_BYTES), and nothing is allocated. Calls that overlap
+        on one GPU share that scratch and race."""
+        self.check_operands(a, b, c, None, bias)
+        st = self._default_stream(stream, a, b, c)
+        _check(lib().tb_gemm_launch_noalloc(self._h, _ptr(a), _ptr(b), _ptr(c),
+                                            _ptr(bias), st))
 
     def bind(self, a, b, c, workspace=None, stream=None, bias=None):
         """A zero-argument launcher for repeated launches on the same buffers

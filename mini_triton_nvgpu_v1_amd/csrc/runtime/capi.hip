@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -185,51 +186,48 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
 
 } // namespace tbrt
 
-extern "C" {
+// ---- the scratch of tb_gemm_launch_noalloc --------------------------------
+// The split-K workspace of the entry point that allocates nothing: a static
+// device array of TB_NOALLOC_SCRATCH_BYTES, one copy per GPU, held until the
+// process ends. Host code never passes `scratch` itself to a kernel (in host
+// code the name is a host-side stand-in, not a device address): the device
+// address comes from hipGetSymbolAddress, once per device with that device
+// current, and is kept per device. Calls on one GPU share its array; each
+// call writes every partial its reduction reads, so nothing needs clearing,
+// and calls that overlap on one GPU race.
+static __device__ __align__(256) float scratch[TB_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
-const char *tb_last_error(void) { return g_last_error.c_str(); }
+namespace {
 
-int tb_abi_version(void) { return TB_GFX950_ABI_VERSION; }
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
 
-int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out) {
-  if (!cfg)
-    return fail("tb_desc_create: cfg is NULL");
-  return tbrt::create_desc(*cfg, out);
-}
-
-int tb_desc_get_config(const tb_gemm_desc *desc, tb_gemm_config *out) {
-  if (!desc || !out)
-    return fail("tb_desc_get_config: NULL argument");
-  *out = desc->cfg;
+int scratch_address(void **out) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice"))
+    return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail("tb_gemm_launch_noalloc: device index " + std::to_string(dev) +
+                " beyond the library's table of " + std::to_string(kMaxDevices));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
+                           "hipGetSymbolAddress(scratch)"))
+      return rc;
+    if (!ptr)
+      return fail("tb_gemm_launch_noalloc: hipGetSymbolAddress returned no address");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
   return 0;
 }
 
-const char *tb_desc_kernel_name(const tb_gemm_desc *desc) {
-  return desc && desc->entry ? desc->entry->name : "";
-}
-
-int64_t tb_desc_lds_bytes(const tb_gemm_desc *desc) {
-  return desc ? desc->lds_bytes : 0;
-}
-
-size_t tb_workspace_bytes(const tb_gemm_desc *desc) {
-  return desc ? desc->workspace_bytes : 0;
-}
-
-void tb_desc_free(tb_gemm_desc *desc) { delete desc; }
-
-int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
-                   void *c, void *workspace, void *stream) {
-  if (d && d->cfg.epi_bias != TB_EPI_BIAS_NONE)
-    return fail("tb_gemm_launch: this descriptor adds a bias; pass it through "
-                "tb_gemm_launch_ex");
-  return tb_gemm_launch_ex(d, a, b, c, nullptr, workspace, stream);
-}
-
-int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
-                      void *c, const void *bias, void *workspace, void *stream) {
+static int launch_impl(const tb_gemm_desc *d, const void *a, const void *b, void *c,
+                       const void *bias, void *workspace, void *stream, const char *who) {
   if (!d)
-    return fail("tb_gemm_launch: desc is NULL");
+    return fail(std::string(who) + ": desc is NULL");
   if (!a || !b || !c)
     return fail("tb_gemm_launch: A, B and C must be device pointers");
   // every kernel moves 16-byte vectors from these bases
@@ -302,6 +300,72 @@ int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
       return rc;
   }
   return 0;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *tb_last_error(void) { return g_last_error.c_str(); }
+
+int tb_abi_version(void) { return TB_GFX950_ABI_VERSION; }
+
+int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out) {
+  if (!cfg)
+    return fail("tb_desc_create: cfg is NULL");
+  return tbrt::create_desc(*cfg, out);
+}
+
+int tb_desc_get_config(const tb_gemm_desc *desc, tb_gemm_config *out) {
+  if (!desc || !out)
+    return fail("tb_desc_get_config: NULL argument");
+  *out = desc->cfg;
+  return 0;
+}
+
+const char *tb_desc_kernel_name(const tb_gemm_desc *desc) {
+  return desc && desc->entry ? desc->entry->name : "";
+}
+
+int64_t tb_desc_lds_bytes(const tb_gemm_desc *desc) {
+  return desc ? desc->lds_bytes : 0;
+}
+
+size_t tb_workspace_bytes(const tb_gemm_desc *desc) {
+  return desc ? desc->workspace_bytes : 0;
+}
+
+void tb_desc_free(tb_gemm_desc *desc) { delete desc; }
+
+int tb_gemm_launch(const tb_gemm_desc *d, const void *a, const void *b,
+                   void *c, void *workspace, void *stream) {
+  if (d && d->cfg.epi_bias != TB_EPI_BIAS_NONE)
+    return fail("tb_gemm_launch: this descriptor adds a bias; pass it through "
+                "tb_gemm_launch_ex");
+  return tb_gemm_launch_ex(d, a, b, c, nullptr, workspace, stream);
+}
+
+int tb_gemm_launch_ex(const tb_gemm_desc *d, const void *a, const void *b,
+                      void *c, const void *bias, void *workspace, void *stream) {
+  return launch_impl(d, a, b, c, bias, workspace, stream, "tb_gemm_launch");
+}
+
+int tb_gemm_launch_noalloc(const tb_gemm_desc *d, const void *a, const void *b,
+                           void *c, const void *bias, void *stream) {
+  if (!d)
+    return fail("tb_gemm_launch_noalloc: desc is NULL");
+  void *ws = nullptr;
+  if (d->workspace_bytes) {
+    if (d->workspace_bytes > (size_t)TB_NOALLOC_SCRATCH_BYTES)
+      return fail("tb_gemm_launch_noalloc: this descriptor needs " +
+                  std::to_string(d->workspace_bytes) +
+                  " bytes of split-K workspace, more than the library's static scratch of " +
+                  std::to_string((size_t)TB_NOALLOC_SCRATCH_BYTES) +
+                  " bytes; use tb_gemm_launch_ex with a caller-provided workspace");
+    if (int rc = scratch_address(&ws))
+      return rc;
+  }
+  return launch_impl(d, a, b, c, bias, ws, stream, "tb_gemm_launch_noalloc");
 }
 
 int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,

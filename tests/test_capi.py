@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_struct_layout(tmp_path):
     """The ctypes mirror of tb_gemm_config matches the C compiler's layout."""
-    assert tb.lib().tb_abi_version() == 3
+    assert tb.lib().tb_abi_version() == 4
     fields = [name for name, _ in tb.GemmConfig._fields_]
     src = tmp_path / "layout.c"
     src.write_text(

@@ -1,0 +1,102 @@
+"""tb_gemm_launch_noalloc: the entry point that allocates nothing.
+
+It is tb_gemm_launch_ex without the workspace argument: a split-K
+descriptor's f32 partials go to the library's static per-GPU scratch
+(TB_NOALLOC_SCRATCH_BYTES). On the GPU it is called through the C ABI and its
+output compared with tb_gemm_launch_ex's (caller-provided workspace) on the
+same inputs: the same kernels summing in the same fixed split order, so the
+results must be bit-identical, and both within the oracle's tolerance. Two
+split-K calls run back to back, the second smaller, so the second reads a
+scratch that still holds the first call's partials. On the CPU: a descriptor
+that needs more than the scratch is refused before any GPU call.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import mini_triton_nvgpu_v1_amd as tb
+import oracle
+from mini_triton_nvgpu_v1_amd import configs
+
+RTOL = 1e-2
+
+
+def _noalloc(desc, a, b, c, bias=None, stream=None):
+    """tb_gemm_launch_noalloc through ctypes, on raw device addresses."""
+    L = tb.lib()
+    rc = L.tb_gemm_launch_noalloc(desc.handle, a.data_ptr(), b.data_ptr(), c.data_ptr(),
+                                  None if bias is None else bias.data_ptr(),
+                                  None if stream is None else stream.cuda_stream)
+    if rc:
+        raise tb.TbError(L.tb_last_error().decode())
+
+
+def test_noalloc_refuses_a_workspace_beyond_the_scratch():
+    """1024 x 1024 x 4096 with 16 splits needs 64 MiB of partials, more than
+    the 32 MiB scratch: a clear error, before any GPU call."""
+    cfg = configs.SPLIT_K.direct_config()
+    cfg.m = cfg.n = cfg.lda = cfg.ldb = cfg.ldc = 1024
+    cfg.k = 4096
+    cfg.lda = 4096
+    cfg.split_k = 16
+    cfg.num_programs = (1024 // cfg.block_m) * (1024 // cfg.block_n) * 16
+    d = tb.GemmDesc.from_config(cfg)
+    assert d.workspace_bytes == 16 * 1024 * 1024 * 4 > tb.NOALLOC_SCRATCH_BYTES
+    L = tb.lib()
+    assert L.tb_gemm_launch_noalloc(d.handle, 16, 16, 16, None, None) != 0
+    msg = L.tb_last_error().decode()
+    assert "more than the library's static scratch of 33554432 bytes" in msg, msg
+
+
+def _case(name, M, N, K, split, seed, bias=None, act=""):
+    w = configs.Workload(name, M, N, K, seed, configs.UNIFORM, (128, 64, 64),
+                         num_waves=4, stages=3, split_k=split,
+                         exact_tile=M % 128 == 0 and N % 64 == 0 and K % 64 == 0,
+                         bias=bias or "", activation=act)
+    return w
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_the_workspace_entry_point(device):
+    import torch
+    stream = torch.cuda.current_stream(device)
+    cases = [
+        # the BASELINE split-K workload (8 MiB of partials), then a smaller
+        # ragged one that reuses the front of the same scratch, then a fused
+        # bias + GELU split-K, then a descriptor with no workspace at all
+        _case("splitk_512x512x16384", 512, 512, 16384, 8, 0x5EED0005),
+        _case("splitk_ragged_200x120x2000", 200, 120, 2000, 3, 0x5EED0D01),
+        _case("splitk_fused_256x192x4096", 256, 192, 4096, 4, 0x5EED0D02, bias="f32",
+              act="gelu_tanh"),
+        configs.SMOKE,
+    ]
+    for w in cases:
+        print(f"no-alloc case {w.name}", flush=True)
+        desc = tb.plan_from_mlir(w.mlir())
+        assert desc.workspace_bytes <= tb.NOALLOC_SCRATCH_BYTES
+        A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
+        dA = torch.from_numpy(A).to(device)
+        dB = torch.from_numpy(B).to(device)
+        bias_h = bias_d = None
+        if w.bias:
+            bias_h = oracle.fill_f16(1, w.N, w.seed ^ 0xB1A5, oracle.UNIFORM, 1.0)
+            bias_h = bias_h.reshape(w.N).astype(np.float32)
+            bias_d = torch.from_numpy(bias_h).to(device)
+        c_ref = torch.full((w.M, w.N), float("nan"), dtype=torch.float16, device=device)
+        c_new = torch.full((w.M, w.N), float("nan"), dtype=torch.float16, device=device)
+        ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=device)
+              if desc.workspace_bytes else None)
+        desc.launch(dA, dB, c_ref, ws, stream=stream, bias=bias_d)
+        _noalloc(desc, dA, dB, c_new, bias_d, stream)
+        torch.cuda.synchronize(device)
+        got_ref, got_new = c_ref.cpu().numpy(), c_new.cpu().numpy()
+        assert np.array_equal(got_new.view(np.uint16), got_ref.view(np.uint16)), (
+            f"{w.name}: tb_gemm_launch_noalloc differs from tb_gemm_launch_ex")
+        ref = oracle.gemm_f64(A, B)
+        if w.bias or w.activation:
+            oracle.epilogue_f64(ref, bias_h, configs.ACTIVATIONS[w.activation])
+        bad, err, worst = oracle.check_tolerance(got_new, ref, rtol=RTOL)
+        print(f"  {desc.kernel_name}: bit-identical, violations={bad} max|err|={err:.3e}",
+              flush=True)
+        assert bad == 0, f"{w.name}: {bad} elements outside tolerance, worst {err} at {worst}"
