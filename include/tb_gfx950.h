@@ -202,6 +202,15 @@ int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
 int tb_kernel_count(void);
 const char *tb_kernel_name(int i);
 
+/* The s_waitcnt depths compiled into kernel instance i: vmcnt at the
+ * prologue's wait, vmcnt at the per-k-tile barrier, and lgkmcnt at that
+ * barrier (-1: none, the compiler orders the LDS reads). The plan's AsyncPlan
+ * states the same numbers (the reference's lowering emits the waits its
+ * AsyncPlan derives, LowerPipelineToNVGPU.cpp:2279-2294); tb_plan_from_mlir
+ * and tb_plan_from_file refuse a plan whose waits differ from the kernel it
+ * binds. */
+int tb_kernel_waits(int i, int32_t *vm_prologue, int32_t *vm_loop, int32_t *lgkm_loop);
+
 int tb_abi_version(void);
 
 #ifdef __cplusplus

@@ -184,6 +184,8 @@ int kernel_count() {
 }
 
 const KernelEntry *kernel_at(int i) {
+  if (i < 0)
+    return nullptr;
   for (auto t : kTables) {
     int n = 0;
     const KernelEntry *e = t(&n);

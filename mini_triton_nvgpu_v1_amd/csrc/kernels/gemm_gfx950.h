@@ -198,6 +198,10 @@ struct KernelEntry {
   KernelKey key;
   const void *fn;
   const char *name;
+  // s_waitcnt depths compiled into the instance: vmcnt at the prologue's
+  // wait, vmcnt at the per-k-tile barrier, lgkmcnt at that barrier (-1: none;
+  // the compiler orders the LDS reads). The plan's AsyncPlan must state them.
+  int vm_prologue, vm_loop, lgkm_loop;
 };
 
 // Registry of compiled instances (defined in the instance files).

@@ -295,6 +295,14 @@ __device__ __forceinline__ void sched_step() {
 // held up the lone wave's issue (1% slower); every 4 or 3 slots measured
 // 0.7% and 1.3% slower than every 5, and the barrier at slot 32 or 48 no
 // faster than at 40.
+// s_waitcnt depths of the 16x16x32 instance: the prologue issues k-tiles 0
+// and 1 whole (16 loads each per lane) and waits for k-tile 0; each
+// barrier waits for every load and LDS read of the wave.
+constexpr int kMfma16LoadsPerThread = 16;
+constexpr int kMfma16VmPrologue = kMfma16LoadsPerThread;
+constexpr int kMfma16VmLoop = 0;
+constexpr int kMfma16LgkmLoop = 0;
+
 template <bool EPI>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
   constexpr int BK = 64, BQ = 40, LS = 5;
@@ -440,7 +448,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     for (int l = 0; l < 16; ++l)
       load(ra1, rb1, 1, S1{}, l);
   }
-  wait_vmcnt<16>();
+  wait_vmcnt<kMfma16VmPrologue>();
   barrier();
 #pragma unroll
   for (int o = 0; o < 24; ++o)
@@ -458,7 +466,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     // k-tile it+1 landed (this wave's part), and this wave's reads of stage
     // S are done (the last A rows of k step 1 are read in k step 0 but only
     // consumed after the barrier, by MFMAs 40..63)
-    wait_vmcnt_lgkm0<0>();
+    static_assert(kMfma16VmLoop == 0 && kMfma16LgkmLoop == 0, "barrier wait below");
+    wait_vmcnt_lgkm0<kMfma16VmLoop>();
     barrier();
     static_assert(64 - BQ == 24, "one read op per slot after the barrier");
     static_for<64 - BQ>([&](auto s_c) {
@@ -1171,11 +1180,16 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
 } // namespace tbk
 
 // One registry entry per instance.
+#define TBK_WAITS(BM, BN, BK, WGM, WGN, ST)                                      \
+  tbk::GemmTile<BM, BN, BK, WGM, WGN, ST>::VM_PROLOGUE,                          \
+      tbk::GemmTile<BM, BN, BK, WGM, WGN, ST>::VM_LOOP, -1
+
 #define TBK_ENTRY(BM, BN, BK, WGM, WGN, OUT, ST)                                 \
   {{BM, BN, BK, WGM, WGN, OUT, ST, 0},                                           \
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST>),                        \
-   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT}
+   "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT, \
+   TBK_WAITS(BM, BN, BK, WGM, WGN, ST)}
 
 #define TBK_OUTS(BM, BN, BK, WGM, WGN, ST)                                      \
   TBK_ENTRY(BM, BN, BK, WGM, WGN, 0, ST), TBK_ENTRY(BM, BN, BK, WGM, WGN, 1, ST), \
@@ -1189,7 +1203,8 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
    reinterpret_cast<const void *>(                                               \
        &tbk::gemm_kernel<BM, BN, BK, WGM, WGN, OUT, ST, -1, true>),              \
    "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out" #OUT \
-   "_epi"}
+   "_epi",                                                                       \
+   TBK_WAITS(BM, BN, BK, WGM, WGN, ST)}
 
 #define TBK_EPI_OUTS(BM, BN, BK, WGM, WGN, ST)                                  \
   TBK_EPI_ENTRY(BM, BN, BK, WGM, WGN, 0, ST),                                   \

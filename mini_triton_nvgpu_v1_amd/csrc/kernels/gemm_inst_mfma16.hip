@@ -7,10 +7,12 @@ namespace tbk {
 static const KernelEntry kMfma16[] = {
     {{256, 256, 64, 2, 2, kOutF16, 2, 0, 1},
      reinterpret_cast<const void *>(&gemm_mfma16<false>),
-     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"},
+     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32", kMfma16VmPrologue, kMfma16VmLoop,
+     kMfma16LgkmLoop},
     {{256, 256, 64, 2, 2, kOutF16, 2, 1, 1},
      reinterpret_cast<const void *>(&gemm_mfma16<true>),
-     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi"}};
+     "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi", kMfma16VmPrologue,
+     kMfma16VmLoop, kMfma16LgkmLoop}};
 const KernelEntry *entries_mfma16(int *n) {
   *n = sizeof(kMfma16) / sizeof(kMfma16[0]);
   return kMfma16;

@@ -429,6 +429,11 @@ void lowerToGfx950(Module &m, const PassOptions &) {
     }
     launch.attrs["config"] = Dict(cfg);
     launch.attrs["kernel"] = Str(kernelInstanceName(g));
+    // the s_waitcnt depths of the AsyncPlan, which the lowering checked
+    // against the instance: vmcnt at the prologue, vmcnt and lgkmcnt at the
+    // per-k-tile barrier (the runtime checks them against the compiled kernel)
+    const InstanceSchedule sched = instanceSchedule(instanceKeyOf(g));
+    launch.attrs["waits"] = Dense({sched.vmPrologue, sched.vmLoop, sched.lgkmLoop});
     launch.attrs["grid"] = Dense({g.num_programs, 1, 1});
     launch.attrs["block"] = Dense({g.num_waves * k.target.threadsPerWarp, 1, 1});
     launch.attrs["lds_bytes"] = I64(k.sharedWorkspace.totalBytes);

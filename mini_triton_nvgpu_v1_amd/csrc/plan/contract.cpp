@@ -179,6 +179,40 @@ static void checkKernelSwizzle(const KernelContract &k) {
                 "the gfx950 kernels");
 }
 
+// The reference's lowering emits exactly the waits its AsyncPlan derives
+// (LowerPipelineToNVGPU.cpp:2279-2294). Here the waits are compiled into
+// the kernel instance, so the lowering refuses a plan whose AsyncPlan states
+// other waits than the instance it binds: its issue schedule, loads per
+// thread, the prologue's vmcnt (k group 0), the per-k-tile barrier's vmcnt
+// (every later group) and lgkmcnt.
+static void checkKernelWaits(const KernelContract &k, const InstanceKey &key) {
+  const InstanceSchedule s = instanceSchedule(key);
+  const AsyncPlan &a = k.async;
+  auto differ = [&](const std::string &what, int64_t plan, int64_t kernel) {
+    throw Error("AsyncPlan " + what + " (" + std::to_string(plan) +
+                ") differs from the kernel instance `" + instanceName(key) + "` (" +
+                std::to_string(kernel) + ")");
+  };
+  if (a.issueSchedule != s.issue)
+    throw Error("AsyncPlan issue schedule `" + a.issueSchedule +
+                "` differs from the kernel instance's `" + s.issue + "`");
+  if (a.loadsPerThread != s.loadsPerThread)
+    differ("loads per thread", a.loadsPerThread, s.loadsPerThread);
+  if (a.prologueTailLoads != s.prologueTailLoads)
+    differ("prologue tail loads", a.prologueTailLoads, s.prologueTailLoads);
+  if (a.waits.empty())
+    throw Error("AsyncPlan has no waits");
+  for (const WaitInfo &w : a.waits) {
+    const int64_t vm = w.groupId == 0 ? s.vmPrologue : s.vmLoop;
+    if (w.vmcntAllowance != vm)
+      differ("vmcnt of the wait for k group " + std::to_string(w.groupId),
+             w.vmcntAllowance, vm);
+    if (w.lgkmcntAllowance != s.lgkmLoop)
+      differ("lgkmcnt of the wait for k group " + std::to_string(w.groupId),
+             w.lgkmcntAllowance, s.lgkmLoop);
+  }
+}
+
 // Reference: LowerPipelineToNVGPU.cpp:2624-2732 (contract -> gpu.func +
 // launch geometry). Here the contract selects a precompiled gfx950 kernel
 // instance and fills its launch configuration.
@@ -251,6 +285,7 @@ tb_gemm_config lowerContractToConfig(const KernelContract &k) {
   if (!hasGfx950Instance(key))
     throw Error("no gfx950 kernel instance `" + instanceName(key) +
                 "` for this contract (see tb-opt --list-instances)");
+  checkKernelWaits(k, key);
   return g;
 }
 

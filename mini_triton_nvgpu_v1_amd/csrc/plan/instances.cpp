@@ -78,6 +78,38 @@ InstanceKey instanceKeyOf(const tb_gemm_config &c) {
   return k;
 }
 
+InstanceSchedule instanceSchedule(const InstanceKey &k) {
+  InstanceSchedule s;
+  if (k.mfma == TB_MFMA_16X16X32) {
+    s.issue = "exact_tile_slots";
+    s.loadsPerThread = 16; // 256x64 + 64x256 halves, 16-byte loads, 256 lanes
+    s.prologueTailLoads = 16;
+    s.refillSpreadSlots = 16 * 5; // one load every 5 MFMA slots from the barrier
+    s.vmPrologue = 16;
+    s.vmLoop = 0;
+    s.lgkmLoop = 0;
+    return s;
+  }
+  const int64_t threads = k.wgm * k.wgn * 64;
+  const int64_t nmfma = (k.bm / k.wgm / 32) * (k.bn / k.wgn / 32); // per 16-deep k step
+  const int64_t lpt = (k.bm * (k.bk / 8) + k.bk * (k.bn / 8)) / threads;
+  s.loadsPerThread = lpt;
+  if (nmfma >= 4) {
+    s.issue = "slot_spread";
+    const int64_t nslot = (k.bk / 16) * nmfma, after = nmfma / 2;
+    s.refillSpreadSlots = k.stages >= 3 ? nslot : nmfma;
+    for (int64_t l = 0; l < lpt; ++l) // load l goes refillSpreadSlots * l / lpt slots in
+      s.prologueTailLoads += s.refillSpreadSlots * l / lpt < after ? 1 : 0;
+  } else {
+    s.issue = "burst";
+    s.prologueTailLoads = lpt;
+  }
+  s.vmPrologue = (k.stages - 2) * lpt + s.prologueTailLoads;
+  s.vmLoop = (k.stages - 2) * lpt;
+  s.lgkmLoop = -1;
+  return s;
+}
+
 std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>
 compiledWaveGrids(int64_t bm, int64_t bn, int64_t bk) {
   std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>> v;

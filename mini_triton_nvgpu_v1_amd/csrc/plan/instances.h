@@ -42,6 +42,26 @@ std::string instanceName(const InstanceKey &k);
 // from C's type, C's initialisation and the reduction; split-K partials take
 // the fused steps in the reduction, so they bind the plain instance.
 InstanceKey instanceKeyOf(const tb_gemm_config &c);
+// How an instance issues its direct-to-LDS loads, and the s_waitcnt depths
+// that follow (the kernel's GemmTile slot geometry, restated on the host):
+//  * "slot_spread": wave tiles of 4+ MFMAs per k step; the k-tile is cut
+//    into MFMA slots and a refill's loads are spread one per slot over
+//    `refillSpreadSlots` slots from the barrier on; the prologue issues
+//    k-tiles 0 .. S-2 whole and the first `prologueTailLoads` loads of k-tile
+//    S-1 (those a refill issues before the next barrier);
+//  * "burst": smaller wave tiles; a refill is issued whole right after the
+//    barrier, and the prologue issues all S k-tiles;
+//  * "exact_tile_slots": the 16x16x32 instance (k-tiles 0 and 1 whole in the
+//    prologue; every barrier waits for all loads and LDS reads).
+// vmcnt at the prologue wait = (S-2) loads-per-thread + prologueTailLoads,
+// vmcnt at the per-k-tile barrier = (S-2) loads-per-thread; lgkmcnt -1 = none.
+struct InstanceSchedule {
+  std::string issue;
+  int64_t loadsPerThread = 0, prologueTailLoads = 0, refillSpreadSlots = 0;
+  int64_t vmPrologue = 0, vmLoop = 0, lgkmLoop = -1;
+};
+InstanceSchedule instanceSchedule(const InstanceKey &k);
+
 // (wave grid, stages) pairs compiled for a block shape on 32x32x16 MFMA.
 std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>
 compiledWaveGrids(int64_t bm, int64_t bn, int64_t bk);

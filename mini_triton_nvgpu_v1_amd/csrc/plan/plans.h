@@ -602,7 +602,9 @@ struct WaitInfo {
           requiredCluster = -1, requiredOrder = -1;
   bool needsBarrier = true;
   std::string reason;
-  int64_t vmcntAllowance = 0; // gfx950: s_waitcnt vmcnt(N) outstanding loads
+  int64_t vmcntAllowance = 0;  // gfx950: s_waitcnt vmcnt(N) outstanding loads
+  int64_t lgkmcntAllowance = -1; // gfx950: s_waitcnt lgkmcnt(N) with the barrier
+                                 // (-1: none; the compiler orders LDS reads)
 };
 struct ReuseFence {
   int64_t viewId = -1, backing = -1, retiringValueId = -1, acquiringValueId = -1,
@@ -615,6 +617,10 @@ struct AsyncPlan {
   std::vector<AsyncGroup> groups;
   std::vector<WaitInfo> waits;
   std::vector<ReuseFence> reuseFences;
+  // gfx950: how the bound kernel instance issues its loads, from which the
+  // waits' depths follow (instances.h, InstanceSchedule)
+  std::string issueSchedule;
+  int64_t loadsPerThread = 0, prologueTailLoads = 0, refillSpreadSlots = 0;
 };
 AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
                           const TransportPlan &tr, const LatencyPlan &lat,

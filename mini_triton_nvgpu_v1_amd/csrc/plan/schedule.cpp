@@ -17,6 +17,7 @@
 // size. Here the model covers a steady-state window of min(k groups, S + 1)
 // groups, which shows every slot's load, reuse and wait once; LoopPlan's
 // iteration_count records the real trip count the kernels run.
+#include "instances.h"
 #include "serialize.h"
 
 #include <algorithm>
@@ -557,6 +558,7 @@ template <class V> void fields(V &v, WaitInfo &w) {
   v("needs_barrier", w.needsBarrier);
   v("reason", w.reason);
   v("vmcnt_allowance", w.vmcntAllowance);
+  v("lgkmcnt_allowance", w.lgkmcntAllowance);
 }
 template <class V> void fields(V &v, ReuseFence &f) {
   v("view_id", f.viewId);
@@ -574,6 +576,10 @@ template <class V> void fields(V &v, AsyncPlan &p) {
   v("groups", p.groups);
   v("waits", p.waits);
   v("reuse_fences", p.reuseFences);
+  v("issue_schedule", p.issueSchedule);
+  v("loads_per_thread", p.loadsPerThread);
+  v("prologue_tail_loads", p.prologueTailLoads);
+  v("refill_spread_slots", p.refillSpreadSlots);
 }
 
 // Loads one thread issues per k group: each 16-byte vector of the A and B
@@ -591,16 +597,39 @@ static int64_t loadsPerThread(const KernelConfig &c, const TransportPlan &tr) {
 // Reference: AsyncPlan.cpp:543-843 (one producer group per stage-owned
 // buffer, a wait at the first-use frontier, reuse fences before a slot is
 // refilled). gfx950: the producers are direct-to-LDS buffer loads, counted
-// per lane by vmcnt; the wait for group g lets the loads of the S - 2 later
-// groups already in flight stay outstanding (s_waitcnt vmcnt((S-2) x loads
-// per thread)), followed by s_barrier so every wave's share has landed.
+// per lane by vmcnt in issue order. The waits' depths are those of the
+// kernel instance the plan binds, which follow from how it issues its loads
+// (InstanceSchedule): at the per-k-tile barrier the loads of the S - 2 later
+// groups stay outstanding (vmcnt((S-2) x loads per thread)); at the
+// prologue's wait also the part of group S-1 the prologue issues. Each wait
+// is followed by s_barrier so every wave's share has landed; the 16x16x32
+// instance also waits lgkmcnt(0) there (its LDS reads of the stage the
+// barrier frees have returned).
 AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
                           const TransportPlan &tr, const LatencyPlan &,
                           const PipelinePlan &pp) {
   AsyncPlan p;
   const int64_t S = c.requestedStages, lpt = loadsPerThread(c, tr);
-  if ((S - 1) * lpt > 63)
+  InstanceKey key;
+  const auto grid = deriveWaveGrid(c, 32, 32);
+  key.bm = c.blockM;
+  key.bn = c.blockN;
+  key.bk = c.blockK;
+  key.wgm = grid.first;
+  key.wgn = grid.second;
+  key.stages = S;
+  key.mfma = c.mmaKind == MmaKind::Mfma16x16x32F16 ? TB_MFMA_16X16X32 : TB_MFMA_32X32X16;
+  const InstanceSchedule sched = instanceSchedule(key);
+  if (sched.loadsPerThread != lpt)
+    throw Error("transport plan loads per thread (" + std::to_string(lpt) +
+                ") disagree with the kernel's issue schedule (" +
+                std::to_string(sched.loadsPerThread) + ")");
+  if (sched.vmPrologue > 63)
     throw Error("outstanding loads per lane exceed the vmcnt counter (63)");
+  p.issueSchedule = sched.issue;
+  p.loadsPerThread = lpt;
+  p.prologueTailLoads = sched.prologueTailLoads;
+  p.refillSpreadSlots = sched.refillSpreadSlots;
   std::map<int64_t, const PipelinePlacement *> place;
   for (const PipelinePlacement &pl : pp.placements)
     place[pl.opId] = &pl;
@@ -655,8 +684,11 @@ AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
     w.requiredCluster = pl->cluster;
     w.requiredOrder = pl->order;
     w.needsBarrier = true;
-    w.vmcntAllowance = g.id == 0 ? (S - 1) * lpt : (S - 2) * lpt;
-    w.reason = g.id == 0 ? "prologue: all S slots issued, wait for the first"
+    w.vmcntAllowance = g.id == 0 ? (S - 2) * lpt + sched.prologueTailLoads : (S - 2) * lpt;
+    w.lgkmcntAllowance = sched.lgkmLoop;
+    w.reason = g.id == 0 ? "prologue: k groups 0 .. S-2 and the first " +
+                               std::to_string(sched.prologueTailLoads) +
+                               " loads of group S-1 issued, wait for group 0"
                          : "waited before the previous slot's refill, sharing its barrier";
     p.waits.push_back(w);
   }

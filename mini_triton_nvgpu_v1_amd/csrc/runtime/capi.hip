@@ -44,6 +44,12 @@ namespace tbrt {
 
 void set_error(const std::string &msg) { g_last_error = msg; }
 
+void desc_waits(const tb_gemm_desc *d, int64_t out[3]) {
+  out[0] = d->entry->vm_prologue;
+  out[1] = d->entry->vm_loop;
+  out[2] = d->entry->lgkm_loop;
+}
+
 // Validate a flattened config and bind it to a compiled instance.
 int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
   if (!out)
@@ -384,6 +390,16 @@ int tb_kernel_count(void) { return tbk::kernel_count(); }
 const char *tb_kernel_name(int i) {
   const tbk::KernelEntry *e = tbk::kernel_at(i);
   return e ? e->name : "";
+}
+
+int tb_kernel_waits(int i, int32_t *vm_prologue, int32_t *vm_loop, int32_t *lgkm_loop) {
+  const tbk::KernelEntry *e = tbk::kernel_at(i);
+  if (!e || !vm_prologue || !vm_loop || !lgkm_loop)
+    return fail("tb_kernel_waits: no instance " + std::to_string(i) + " or NULL output");
+  *vm_prologue = e->vm_prologue;
+  *vm_loop = e->vm_loop;
+  *lgkm_loop = e->lgkm_loop;
+  return 0;
 }
 
 } // extern "C"

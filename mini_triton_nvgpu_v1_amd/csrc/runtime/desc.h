@@ -25,4 +25,7 @@ namespace tbrt {
 int create_desc(const tb_gemm_config &c, tb_gemm_desc **out);
 // Sets the thread-local message returned by tb_last_error().
 void set_error(const std::string &msg);
+// The s_waitcnt depths compiled into the descriptor's kernel instance:
+// {vmcnt at the prologue, vmcnt at the per-k-tile barrier, lgkmcnt there}.
+void desc_waits(const tb_gemm_desc *d, int64_t out[3]);
 } // namespace tbrt

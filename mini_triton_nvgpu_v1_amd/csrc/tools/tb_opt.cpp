@@ -36,7 +36,8 @@ void usage() {
   std::printf("usage: tb-opt [input.mlir|-] [-o output] "
               "[--pass-pipeline='builtin.module(...)'] [--<pass>[=<options>]]...\n"
               "       tb-opt --list-passes\n"
-              "       tb-opt --list-instances   (the gfx950 kernels a plan can bind)\n");
+              "       tb-opt --list-instances   (the gfx950 kernels a plan can bind, with the\n"
+              "                                  issue schedule and waits the plan states)\n");
 }
 
 } // namespace
@@ -57,8 +58,13 @@ int main(int argc, char **argv) {
         return 0;
       }
       if (a == "--list-instances") {
-        for (const tb::InstanceKey &k : tb::gfx950Instances())
-          std::printf("%s\n", tb::instanceName(k).c_str());
+        // name, then the s_waitcnt depths the plan states for it
+        for (const tb::InstanceKey &k : tb::gfx950Instances()) {
+          const tb::InstanceSchedule s = tb::instanceSchedule(k);
+          std::printf("%s %s vmcnt_prologue=%lld vmcnt_loop=%lld lgkmcnt_loop=%lld\n",
+                      tb::instanceName(k).c_str(), s.issue.c_str(), (long long)s.vmPrologue,
+                      (long long)s.vmLoop, (long long)s.lgkmLoop);
+        }
         return 0;
       }
       if (a == "-o") {

@@ -30,3 +30,7 @@ module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {
 // CHECK-SAME: xcd_remap = 8 : i64
 // CHECK-SAME: kernel = "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
 // CHECK-SAME: lds_bytes = 131072 : i64
+// The waits the AsyncPlan states and the lowering checked against this
+// instance: vmcnt(16) in the prologue (k-tile 1's 16 loads per lane still in
+// flight), vmcnt(0) lgkmcnt(0) at each k-tile's barrier.
+// CHECK-SAME: waits = array<i64: 16, 0, 0>

@@ -243,14 +243,106 @@ def test_cleanup_layout_conversions():
     assert "tb.matmul %A, %B, %C" in out
 
 
-def test_tb_opt_instance_table_equals_the_kernel_registry():
-    """tb-opt carries the instance table without the kernels; it lists
-    exactly the instances compiled into libtb_gfx950.so, by the same names."""
+def _listed_instances():
+    """tb-opt --list-instances: name -> (issue schedule, vmcnt prologue,
+    vmcnt loop, lgkmcnt loop) from the host-side table."""
     p = subprocess.run([str(TB_OPT), "--list-instances"], capture_output=True,
                        text=True, timeout=60, check=True)
-    listed = p.stdout.split()
-    assert len(listed) == len(set(listed))
-    assert sorted(listed) == sorted(tb.kernel_names())
+    out = {}
+    for line in p.stdout.splitlines():
+        name, issue, *kv = line.split()
+        vals = dict(x.split("=") for x in kv)
+        assert name not in out
+        out[name] = (issue, int(vals["vmcnt_prologue"]), int(vals["vmcnt_loop"]),
+                     int(vals["lgkmcnt_loop"]))
+    return out
+
+
+def _compiled_waits():
+    """The registry of libtb_gfx950.so: name -> the s_waitcnt depths compiled
+    into the kernel (the kernel template's own constants)."""
+    import ctypes
+    L = tb.lib()
+    L.tb_kernel_waits.argtypes = [ctypes.c_int] + [ctypes.POINTER(ctypes.c_int32)] * 3
+    out = {}
+    for i, name in enumerate(tb.kernel_names()):
+        v = [ctypes.c_int32() for _ in range(3)]
+        assert L.tb_kernel_waits(i, *[ctypes.byref(x) for x in v]) == 0
+        out[name] = tuple(x.value for x in v)
+    return out
+
+
+def test_tb_opt_instance_table_equals_the_kernel_registry():
+    """tb-opt carries the instance table without the kernels; it lists
+    exactly the instances compiled into libtb_gfx950.so, by the same names,
+    and states for each the waits the kernel's own constants compile in
+    (vmcnt at the prologue, vmcnt and lgkmcnt at the per-k-tile barrier)."""
+    listed, compiled = _listed_instances(), _compiled_waits()
+    assert sorted(listed) == sorted(compiled)
+    for name, (issue, vmp, vml, lgkm) in listed.items():
+        assert (vmp, vml, lgkm) == compiled[name], (name, issue)
+    # the three issue schedules all occur, and differ in the prologue wait
+    assert {v[0] for v in listed.values()} == {"slot_spread", "burst", "exact_tile_slots"}
+    assert listed["tb_gemm_gfx950_256x256x64_w4x2_s2_out0"][1:] == (4, 0, -1)
+    assert listed["tb_gemm_gfx950_128x64x64_w4x1_s3_out1"][:2] == ("burst", 12)
+    assert listed["tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"][1:] == (16, 0, 0)
+    L = tb.lib()
+    import ctypes
+    x = ctypes.c_int32()
+    assert L.tb_kernel_waits(-1, ctypes.byref(x), ctypes.byref(x), ctypes.byref(x)) != 0
+    assert L.tb_kernel_waits(len(compiled), ctypes.byref(x), ctypes.byref(x),
+                             ctypes.byref(x)) != 0
+
+
+def _async_waits(text):
+    """The sealed mainline's tb.async_plan: (issue_schedule, loads_per_thread,
+    prologue_tail_loads, [(group, vmcnt, lgkmcnt), ...]) read from the IR."""
+    out = tb_opt(text, f"--pass-pipeline={MAINLINE}").stdout
+    body = out[out.index("tb.async_plan"):]
+    issue = re.search(r'issue_schedule = "(\w+)"', body).group(1)
+    lpt = int(re.search(r"loads_per_thread = (\d+)", body).group(1))
+    tail = int(re.search(r"prologue_tail_loads = (\d+)", body).group(1))
+    waits = [(int(g), int(vm), int(lg)) for g, lg, vm in re.findall(
+        r"group_id = (\d+) : i64, lgkmcnt_allowance = (-?\d+) : i64.*?"
+        r"vmcnt_allowance = (\d+) : i64", body)]
+    return issue, lpt, tail, waits
+
+
+@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+def test_async_plan_states_the_bound_kernels_waits(w):
+    """The AsyncPlan's waits are those compiled into the kernel the plan
+    binds: vmcnt at the prologue (k group 0), vmcnt at every later barrier,
+    lgkmcnt there (reference: the lowering emits the AsyncPlan's waits,
+    LowerPipelineToNVGPU.cpp:2279-2294)."""
+    issue, lpt, tail, waits = _async_waits(w.mlir())
+    assert waits and waits[0][0] == 0
+    name = tb.plan_from_mlir(w.mlir()).kernel_name
+    vmp, vml, lgkm = _compiled_waits()[name]
+    assert _listed_instances()[name][0] == issue
+    for g, vm, lg in waits:
+        assert vm == (vmp if g == 0 else vml), (name, g, vm)
+        assert lg == lgkm, (name, g, lg)
+    assert vmp == (w.stages - 2) * lpt + tail
+
+
+def test_lowering_refuses_waits_that_differ_from_the_kernel():
+    """A sealed mainline whose AsyncPlan states another wait depth than the
+    instance it binds is refused by the lowering, as is one whose lowered
+    launch op carries waits the compiled kernel does not have."""
+    w = configs.ROOFLINE
+    sealed = tb_opt(w.mlir(), f"--pass-pipeline={MAINLINE}").stdout
+    tampered = re.sub(r"vmcnt_allowance = 16 : i64", "vmcnt_allowance = 8 : i64", sealed,
+                      count=1)
+    assert tampered != sealed
+    p = tb_opt(tampered, "--tb-lower-pipeline-to-gfx950", check=False)
+    assert p.returncode == 1 and "AsyncPlan vmcnt of the wait for k group 0 (8)" in p.stderr
+    with pytest.raises(tb.TbError, match="AsyncPlan vmcnt"):
+        tb.plan_from_mlir(tampered)
+    lowered = tb_opt(sealed, "--tb-lower-pipeline-to-gfx950").stdout
+    assert "waits = array<i64: 16, 0, 0>" in lowered
+    bad = lowered.replace("waits = array<i64: 16, 0, 0>", "waits = array<i64: 16, 0, -1>")
+    with pytest.raises(tb.TbError, match="differ from the compiled kernel"):
+        tb.plan_from_mlir(bad)
 
 
 # every block shape with an instance list, 1 to 8 waves, 2 to 4 stages,
