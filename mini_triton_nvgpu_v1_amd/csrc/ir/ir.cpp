@@ -1,5 +1,6 @@
 // Parser and printer of the tb IR subset.
 #include "ir.h"
+#include "verify.h"
 
 #include <cctype>
 #include <sstream>
@@ -205,6 +206,7 @@ Module parseModule(const std::string &text) {
     m.funcs.push_back(parseFunc(c));
   if (!c.eof())
     c.fail("trailing text after module");
+  verifyModule(m); // as MLIR verifies a module after parsing it
   return m;
 }
 

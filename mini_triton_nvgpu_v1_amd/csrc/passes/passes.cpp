@@ -4,6 +4,7 @@
 // the reference passes do (lib/Transforms/*.cpp).
 #include "passes.h"
 #include "../plan/instances.h"
+#include "../ir/verify.h"
 
 #include "../plan/contract.h"
 #include "../plan/plans.h"
@@ -100,6 +101,8 @@ void buildProgramMapping(Module &m, const PassOptions &) {
     op.attrs["tb.program_mapping_plan"] = buildProgramMappingPlanAttr(pm);
     op.attrs["tb.reduction_plan"] = buildReductionPlanAttr(rd);
     op.attrs["tb.persistent_work_plan"] = buildPersistentWorkPlanAttr(pw);
+    // the launch's CTA count as module context (BuildProgramMappingPlan.cpp:67-72)
+    m.attrs[kNumCTAs] = I64(pm.numCTAs);
   });
 }
 
@@ -584,6 +587,7 @@ void runPass(Module &m, const PassSpec &p) {
     if (p.name == e.name) {
       try {
         e.fn(m, p.options);
+        verifyModule(m); // after every pass, as MLIR's pass manager does
       } catch (const Error &err) {
         throw Error(p.name + ": " + err.what());
       }

@@ -205,20 +205,20 @@ BufferModel deriveBufferModel(const KernelConfig &c, const EncodingPlan &e,
                                false, {c.problemK, c.problemN}),
                        1, false, "b_global");
   int64_t aS = backing(BufferRole::OperandA,
-                       memdesc({c.blockM, c.blockK}, "f16", aSh, "shared", true,
+                       memdesc({S, c.blockM, c.blockK}, "f16", aSh, "shared", true,
                                {S, c.blockM, c.blockK}),
                        S, true, "a_shared_ring");
   int64_t bS = backing(BufferRole::OperandB,
-                       memdesc({c.blockK, c.blockN}, "f16", bSh, "shared", true,
+                       memdesc({S, c.blockK, c.blockN}, "f16", bSh, "shared", true,
                                {S, c.blockK, c.blockN}),
                        S, true, "b_shared_ring");
   int64_t aR = backing(BufferRole::OperandA,
-                       memdesc({wtM, rw.instructionK}, "f16",
+                       memdesc({2, wtM, rw.instructionK}, "f16",
                                e.encodings.at(e.aDot).encodingAttr, "registers",
                                true, {2, wtM, rw.instructionK}),
                        2, true, "a_fragments");
   int64_t bR = backing(BufferRole::OperandB,
-                       memdesc({rw.instructionK, wtN}, "f16",
+                       memdesc({2, rw.instructionK, wtN}, "f16",
                                e.encodings.at(e.bDot).encodingAttr, "registers",
                                true, {2, rw.instructionK, wtN}),
                        2, true, "b_fragments");

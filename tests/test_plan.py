@@ -217,10 +217,11 @@ def test_verifier_catches_tampering():
     bad = sealed.replace(f"async_groups = {n} : i64", f"async_groups = {n + 1} : i64")
     p = tb_opt(bad, verify, check=False)
     assert p.returncode == 1 and "async_groups" in p.stderr
-    # a refill scheduled before the last read of its slot
+    # a refill moved in front of the reads of its slot: the op verifier
+    # (TBOps.cpp:253-258) refuses the clusters' order as the module is read
     bad = re.sub(r"(tb\.async_issue_cluster \{cluster = )2", r"\g<1>0", sealed, count=4)
     p = tb_opt(bad, verify, check=False)
-    assert p.returncode == 1 and "contract" in p.stderr
+    assert p.returncode == 1 and "clusters must stay ordered by stage/cluster" in p.stderr
     # the lowering refuses an LDS encoding the kernels do not implement
     bad = sealed.replace("perPhase = 2, maxPhase = 8", "perPhase = 1, maxPhase = 8")
     assert bad != sealed
@@ -228,19 +229,151 @@ def test_verifier_catches_tampering():
     assert p.returncode == 1 and "swizzle" in p.stderr
 
 
+CGA = "#tb.cga<ctasPerCGA = [1, 1, 1], ctaSplitNum = [1, 1, 1], ctaOrder = [0, 1, 2]>"
+
+
+def _memdesc(order, shape=(64, 32), space="global", alloc=None):
+    enc = (f"#tb.blocked<sizePerThread = [1, 1], threadsPerWarp = [32, 1], "
+           f"warpsPerCTA = [1, 1], order = [{order}], cga = {CGA}>")
+    alloc = alloc or shape
+    return (f"!tb.memdesc<shape = [{shape[0]}, {shape[1]}], elementType = f16, "
+            f"encoding = {enc}, memorySpace = \"{space}\", mutableMemory = true, "
+            f"allocShape = [{alloc[0]}, {alloc[1]}]>")
+
+
 def test_cleanup_layout_conversions():
+    """tb-cleanup-layout-conversions (CleanupLayoutConversions.cpp:21-54)
+    folds a conversion back to its source's source: row -> col -> row is the
+    source itself (the reference's examples/layout_convert_roundtrip.mlir),
+    and a dead conversion goes away; a conversion to another layout stays."""
+    row, col = _memdesc("1, 0"), _memdesc("0, 1")
     text = (
-        'module attributes {"tb.num-warps" = 4 : i64, "tb.requested-stages" = 2 : i64} {\n'
-        "  func.func @kernel(%A: memref<64x32xf16>, %B: memref<32x64xf16>, %C: memref<64x64xf16>) {\n"
-        "    %0 = tb.convert_layout %A : (memref<64x32xf16>) -> memref<64x32xf16>\n"
-        "    %1 = tb.convert_layout %B : (memref<32x64xf16>) -> memref<32x64xf16, strided<[64, 1]>>\n"
-        "    %2 = tb.convert_layout %1 : (memref<32x64xf16, strided<[64, 1]>>) -> memref<32x64xf16>\n"
-        "    %3 = tb.convert_layout %C : (memref<64x64xf16>) -> memref<64x64xf16, strided<[64, 1]>>\n"
-        "    tb.matmul %0, %2, %C {block_m = 64 : i64, block_n = 64 : i64, block_k = 32 : i64, exact_tile = true} : memref<64x32xf16>, memref<32x64xf16>, memref<64x64xf16>\n"
-        "    return\n  }\n}\n")
+        "module {\n"
+        f"  func.func @f(%src: {row}) -> {col} {{\n"
+        f"    %0 = tb.convert_layout %src : ({row}) -> {col}\n"
+        f"    %1 = tb.convert_layout %0 : ({col}) -> {row}\n"
+        f"    %2 = tb.convert_layout %1 : ({row}) -> {col}\n"
+        f"    %3 = tb.convert_layout %src : ({row}) -> {col}\n"
+        f"    return %2 : {col}\n  }}\n}}\n")
     out = tb_opt(text, "--tb-cleanup-layout-conversions").stdout
-    assert "tb.convert_layout" not in out
-    assert "tb.matmul %A, %B, %C" in out
+    assert out.count("tb.convert_layout") == 1, out
+    assert "%2 = tb.convert_layout %src" in out and "return %2" in out
+    ex = ROOT.parent / "reference" / "examples" / "layout_convert_roundtrip.mlir"
+    if ex.exists():  # the reference's example, where this container has it
+        out = tb_opt(ex.read_text(), "--tb-cleanup-layout-conversions").stdout
+        assert "tb.convert_layout" not in out and "return %src" in out
+
+
+SHARED_OK = ("#tb.shared<order = [1, 0], perPhase = 1, maxPhase = 4, transposed = false, "
+             f"swizzlingByteWidth = 64, cga = {CGA}>")
+# (name, module text, expected diagnostic): each attribute, type and op rule of
+# the reference's verifiers (TBAttrs.cpp:47-195, TBTypes.cpp:16-46,
+# TBOps.cpp:16-60, :128-182), plus the gfx950 second XOR term.
+IR_ERRORS = [
+    ("shared_negative_phase",
+     SHARED_OK.replace("perPhase = 1, maxPhase = 4", "perPhase = 0, maxPhase = -3"),
+     "per_phase and max_phase must be non-negative"),
+    ("shared_negative_width",
+     SHARED_OK.replace("swizzlingByteWidth = 64", "swizzlingByteWidth = -7"),
+     "swizzling_byte_width must be non-negative"),
+    ("shared_no_cga",
+     SHARED_OK.replace(f", cga = {CGA}", ""), "expected parameter `cga`"),
+    ("shared_bad_order", SHARED_OK.replace("order = [1, 0]", "order = [1, 1]"),
+     "order must not contain duplicates"),
+    ("shared_empty_order", SHARED_OK.replace("order = [1, 0]", "order = []"),
+     "shared encoding must have non-empty order"),
+    ("shared_padding_rank",
+     SHARED_OK[:-1] + ", paddingIntervals = [32, 32], paddings = [8]>",
+     "padding_intervals and paddings must have same rank"),
+    ("shared_second_term_too_wide",
+     SHARED_OK[:-1] + ", secondPerPhase = 8, secondMaxPhase = 4, secondSwizzlingByteWidth = 32>",
+     "second XOR term must permute whole 16-byte chunks"),
+    ("cga_rank", CGA.replace("ctaOrder = [0, 1, 2]", "ctaOrder = [0, 1]"),
+     "cga encoding must carry rank-3"),
+    ("cga_positive", CGA.replace("ctasPerCGA = [1, 1, 1]", "ctasPerCGA = [1, 0, 1]"),
+     "ctas_per_cga entries must be positive"),
+    ("blocked_rank",
+     f"#tb.blocked<sizePerThread = [1, 4], threadsPerWarp = [32], warpsPerCTA = [1, 1], "
+     f"order = [1, 0], cga = {CGA}>", "size_per_thread/threads_per_warp rank mismatch"),
+    ("semantic_contiguous",
+     "#tb.semantic_layout<order = [1, 0], strides = [64, 1], zeroOffset = true, "
+     "hasStaticStrides = true, unitStrideOnMinor = false, contiguous = true>",
+     "contiguous=true requires unitStrideOnMinor=true"),
+    ("semantic_static_strides",
+     "#tb.semantic_layout<order = [1, 0], strides = [64, 0], zeroOffset = true, "
+     "hasStaticStrides = true, unitStrideOnMinor = true, contiguous = true>",
+     "static strides must be positive"),
+    ("mfma_instr_rank",
+     f"#tb.amd_mfma<versionMajor = 4, versionMinor = 0, warpsPerCTA = [2, 2], "
+     f"instrShape = [32, 32], isTransposed = true, cga = {CGA}>",
+     "instr_shape must have rank 3"),
+    ("dot_operand_index",
+     f"#tb.dot_operand<operandIndex = 2, parent = #tb.amd_mfma<versionMajor = 4, "
+     f"versionMinor = 0, warpsPerCTA = [2, 2], instrShape = [32, 32, 16], "
+     f"isTransposed = true, cga = {CGA}>, kWidth = 8>", "operand_index must be 0 or 1"),
+    ("unknown_attr", "#tb.swizzled<order = [1, 0]>", "unknown tb attribute `#tb.swizzled`"),
+]
+
+
+@pytest.mark.parametrize("name,attr,msg", IR_ERRORS, ids=[e[0] for e in IR_ERRORS])
+def test_ir_attribute_verifiers(name, attr, msg):
+    """A malformed #tb attribute is refused when the module is read, by
+    tb-opt and by tb_plan_from_mlir, with the reference's diagnostic."""
+    text = f"#bad = {attr}\n" + matmul_module()
+    p = tb_opt(text, "--tb-verify-scope", check=False)
+    assert p.returncode == 1 and msg in p.stderr, p.stderr
+    with pytest.raises(tb.TbError, match=re.escape(msg)):
+        tb.plan_from_mlir(text)
+
+
+def test_ir_type_and_op_verifiers():
+    """!tb.memdesc (TBTypes.cpp:16-46) and the ops (TBOps.cpp): shapes,
+    memory spaces, conversion legality, matmul operands and attributes."""
+    row, col = _memdesc("1, 0"), _memdesc("0, 1")
+    cases = [
+        (_memdesc("1, 0", space="local"), "memory_space must be one of global/shared/registers"),
+        (_memdesc("1, 0", alloc=(64, 0)), "alloc_shape dimensions must be positive"),
+        (row.replace("#tb.blocked<sizePerThread = [1, 1], threadsPerWarp = [32, 1], "
+                     "warpsPerCTA = [1, 1], order = [1, 0]", "#tb.shared<order = [1, 0], "
+                     "perPhase = 1, maxPhase = 1, transposed = false, swizzlingByteWidth = 16")
+                .replace(f", cga = {CGA}>, memorySpace", f", cga = {CGA}>, memorySpace"),
+         "shared encoding requires shared memory_space"),
+    ]
+    for ty, msg in cases:
+        text = f"module {{\n  func.func @f(%x: {ty}) {{\n    return\n  }}\n}}\n"
+        p = tb_opt(text, "--tb-cleanup-layout-conversions", check=False)
+        assert p.returncode == 1 and msg in p.stderr, (msg, p.stderr)
+    convs = [
+        (row, row, "layout conversion must change encoding or alloc_shape"),
+        (row, _memdesc("0, 1", shape=(32, 64)), "logical shapes must match"),
+        (row, _memdesc("0, 1", space="shared"), "memory spaces must match"),
+    ]
+    for src, dst, msg in convs:
+        text = (f"module {{\n  func.func @f(%x: {src}) {{\n"
+                f"    %0 = tb.convert_layout %x : ({src}) -> {dst}\n    return\n  }}\n}}\n")
+        p = tb_opt(text, "--tb-cleanup-layout-conversions", check=False)
+        assert p.returncode == 1 and msg in p.stderr, (msg, p.stderr)
+    text = matmul_module().replace("tb.convert_layout", "")
+    ops = [
+        (text.replace("block_m = 64", "block_m = 0"), "block sizes must be positive"),
+        (text.replace("exact_tile = true", "exact_tile = true, group_m = 0 : i64"),
+         "group_m must be positive"),
+        (text.replace("%C: memref<64x64xf16>", "%C: memref<64x64xbf16>")
+             .replace("memref<64x64xf16>\n", "memref<64x64xbf16>\n"),
+         "expected fp16 x fp16 -> fp32"),
+        (text.replace("%B: memref<32x64xf16>", "%B: memref<16x64xf16>")
+             .replace(", memref<32x64xf16>,", ", memref<16x64xf16>,"),
+         "expected A:[M,K], B:[K,N], C:[M,N] operand shapes"),
+    ]
+    for t, msg in ops:
+        p = tb_opt(t, "--tb-verify-scope", check=False)
+        assert p.returncode == 1 and msg in p.stderr, (msg, p.stderr)
+    # the sealed mainline keeps the reference's structural rules
+    sealed = tb_opt(matmul_module(), f"--pass-pipeline={MAINLINE}").stdout
+    assert '"tb.num-ctas" = 1 : i64' in sealed
+    p = tb_opt(sealed.replace('"tb.num-ctas" = 1 : i64, ', ""), "--tb-verify-scope",
+               check=False)
+    assert p.returncode == 1 and "requires module attr `tb.num-ctas`" in p.stderr
 
 
 def _listed_instances():
