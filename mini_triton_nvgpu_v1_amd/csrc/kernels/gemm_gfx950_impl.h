@@ -204,6 +204,9 @@ struct GemmTile {
   static constexpr int EPI_CPR = EPI_ROWB / 16;    // 16-byte chunks per row
   static constexpr int EPI_RPP = 256 / EPI_ROWB;   // rows per 256-byte bank period
   static constexpr int EPI_RPI = 64 / EPI_CPR;     // rows per 64-lane read
+  // row bit that swaps a staged chunk's 8-byte halves (the one the chunk XOR
+  // leaves out of a 16-row quarter wave's 128-byte write window)
+  static constexpr int EPI_HALF_BIT = EPI_RPP == 1 ? 3 : 0;
   static constexpr bool STAGED_F16_EPILOGUE =
       SLOTTED && (WTN == 64 || WTN == 128) && WTM * WTN <= 8192 &&
       NW * WTM * EPI_ROWB <= LDS_BYTES;
@@ -315,16 +318,22 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const int nk = p.K / BK;
 
   // Direct loads: round l of wave w fills 1 KiB at slot + l * 4 KiB + w * 1 KiB
-  // (A rows 32l + 8w .. +7; B k-rows 8l + 2w, +1). The swizzle phase repeats
-  // every 16 A rows and every 4 B rows, so a lane fetches the same logical
-  // chunk in every round and only the scalar offset moves.
+  // (A rows 32l + 8w .. +7; B k-rows 8l + 2w, +1). B's 16-byte chunk c of
+  // row k sits at c ^ 4 (k % 4) ^ 2 ((k / 8) % 2) (the plan's B encoding:
+  // the first term over 64-byte segments, the second over 32-byte units; see
+  // the fragment reads). The A phase repeats every 16 rows and the B phase
+  // every 16 k rows, i.e. every 2 rounds, so a lane fetches one logical
+  // chunk in every A round and one per round parity in B; only the scalar
+  // offset moves.
   const int a_row0 = (wave * 64 + lane) >> 3;
   const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
   const uint32_t a_voff = ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + a_lc * 8) * 2u;
-  const int b_row0 = (wave * 64 + lane) >> 5;
+  const int b_row0 = (wave * 64 + lane) >> 5; // 0 .. 7: (k / 8) % 2 = round % 2
   const int b_lc = (lane & 31) ^ (4 * (b_row0 & 3));
-  const uint32_t b_voff =
+  const uint32_t b_voff0 =
       ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + b_lc * 8)) * 2u;
+  const uint32_t b_voff1 =
+      ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + (b_lc ^ 2) * 8)) * 2u;
   const uint32_t a_round = 32u * (uint32_t)p.lda * 2u, b_round = 8u * (uint32_t)p.ldb * 2u;
   const uint32_t a_ktile = BK * 2u, b_ktile = BK * 2u * (uint32_t)p.ldb;
   const uint32_t a_bytes = (uint32_t)p.M * (uint32_t)p.lda * 2u;
@@ -341,7 +350,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
           load_lds16_at<base + L * 4096u>(ra, wlds, a_voff,
                                           (uint32_t)kt * a_ktile + L * a_round);
         else
-          load_lds16_at<base + B_AT + (L - 8) * 4096u>(rb, wlds, b_voff,
+          load_lds16_at<base + B_AT + (L - 8) * 4096u>(rb, wlds, (L & 1) ? b_voff1 : b_voff0,
                                                        (uint32_t)kt * b_ktile +
                                                            (L - 8) * b_round);
       }
@@ -354,8 +363,11 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // a_base[st][ks] + ii * 2 KiB (16 rows of 128 bytes; the row phase
   // (row / 2) % 8 = (l % 16) / 2 is the same for every ii). B tile jj: the 16
   // lanes of group g = l / 16 read k rows 32ks + 8g + l%16/4 (+4 for the
-  // second half), columns 16jj + 4(l%4); with the B swizzle chunk ^ 4(k%4)
-  // the column group lands at 2(jj ^ 2(l%16/4)) 16-byte chunks.
+  // second half), columns 16jj + 4(l%4); with the B swizzle chunk ^ 4(k%4) ^
+  // 2((k/8)%2) the column group lands at 2(jj ^ 2(l%16/4) ^ (g%2)) 16-byte
+  // chunks. A 32-lane LDS cycle serves groups g and g+1, whose rows are 8
+  // apart with equal k % 4: the second term puts them in different 32-byte
+  // units, so the cycle covers the 64 banks once (without it, 2-way conflict).
   const int g = lane >> 4, ta = (lane >> 2) & 3, tb = lane & 3;
   uint32_t a_base[2][2], b_base[2][8];
 #pragma unroll
@@ -367,7 +379,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj)
       b_base[st][jj] = lds0 + st * SLOT + B_AT + (8 * g + ta) * 512 +
-                       (wn * 16 + 2 * (jj ^ (2 * ta)) + (tb >> 1)) * 16 + 8 * (tb & 1);
+                       (wn * 16 + 2 * (jj ^ (2 * ta) ^ (g & 1)) + (tb >> 1)) * 16 +
+                       8 * (tb & 1);
   }
 
   f32x4 acc[8][8];
@@ -501,9 +514,13 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   wait_vmcnt<0>(); // the zero loads past the end have landed too
 
   // f16 C through LDS: each wave's 128x128 tile goes to its own 32 KiB,
-  // 256-byte rows, 16-byte chunk c of row r at c ^ (r % 16) (the 16 rows of a
-  // 16x16 tile then cover the 64 banks once), and comes back as 4 whole rows
-  // per ds_read_b128 / buffer store. The fused steps (bias, activation,
+  // 256-byte rows, 16-byte chunk c of row r at c ^ (r % 8) with the chunk's
+  // two 8-byte halves swapped when (r / 8) is odd, and comes back as 4 whole
+  // rows per ds_read_b128 / buffer store. A ds_write_b64 is served 16 lanes
+  // per cycle from a 128-byte window of the banks (measured: 16 lanes writing
+  // 8-byte pieces 16 bytes apart conflict 2-way, 16 contiguous pieces do
+  // not): the 16 rows a quarter wave writes then land in 16 different 8-byte
+  // slots of that window. The fused steps (bias, activation,
   // clamp) run on each tile's f32 values on their way to LDS. The epilogue's
   // lane-derived addresses come from an opaque copy of the lane index, so the
   // compiler cannot hoist them out of a persistent tile loop and keep them
@@ -543,8 +560,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
         v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
                ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
-        const int chunk = (2 * j + (el >> 5)) ^ (r & 15);
-        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + ((el >> 4) & 1) * 8) = v;
+        const int chunk = (2 * j + (el >> 5)) ^ (r & 7);
+        const int half = ((el >> 4) & 1) ^ ((r >> 3) & 1);
+        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
         if (j & 1)
           __builtin_amdgcn_sched_barrier(0);
       }
@@ -560,7 +578,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 #pragma unroll
   for (int t = 0; t < 32; ++t) {
     const int r = t * 4 + (el >> 4);
-    const u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 15)) * 16));
+    u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 7)) * 16));
+    if ((r >> 3) & 1)
+      v = (u32x4){v[2], v[3], v[0], v[1]};
     const uint32_t off = ((uint32_t)(m0 + wm * 128 + r) * (uint32_t)p.ldc +
                           (uint32_t)(n0 + wn * 128 + 8 * q)) * 2u;
     // non-temporal (nt): C is written once and not read again by this
@@ -929,11 +949,13 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       // scattered over 32 rows write HBM lines partially. Each wave writes
       // its WTM x WTN f16 tile into a private LDS region of EPI_ROWB bytes
       // per row. Row r's 16-byte chunk c sits at c ^ ((r / EPI_RPP) %
-      // EPI_CPR), and the two 8-byte halves of a chunk are swapped when
-      // (r / 16) is odd. The 32 lanes of a ds_write_b64 half (rows r..r+31,
-      // one chunk) then cover all 64 banks once, and so do the 16 lanes of a
-      // ds_read_b128 quarter (whole rows). The tile is read back row by row,
-      // EPI_CPR lanes x 16 bytes per row, and stored EPI_RPI full rows per
+      // EPI_CPR), and the two 8-byte halves of a chunk are swapped when row
+      // bit EPI_HALF_BIT is set. A ds_write_b64 is served 16 lanes per cycle
+      // from a 128-byte window of the banks: the 16 rows of a quarter wave
+      // (one chunk each) then land in 16 different 8-byte slots of the
+      // window, and the 16 lanes of a ds_read_b128 quarter (whole rows)
+      // cover the 64 banks once. The tile is read back row by row, EPI_CPR
+      // lanes x 16 bytes per row, and stored EPI_RPI full rows per
       // instruction.
       __syncthreads(); // every wave drained its loads and finished its reads
       TBK_LDS char *wl =
@@ -955,7 +977,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
             v[1] = (uint32_t)__builtin_bit_cast(uint16_t, h2) |
                    ((uint32_t)__builtin_bit_cast(uint16_t, h3) << 16);
             const int chunk = (4 * j + g) ^ ((r / T::EPI_RPP) & (T::EPI_CPR - 1));
-            const int half = khalf ^ ((r >> 4) & 1);
+            const int half = khalf ^ ((r >> T::EPI_HALF_BIT) & 1);
             *(TBK_LDS u32x2 *)(wl + r * T::EPI_ROWB + chunk * 16 + half * 8) = v;
           }
           __builtin_amdgcn_sched_barrier(0); // one 32x32 tile at a time
@@ -969,7 +991,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         const int r = it2 * T::EPI_RPI + lane / T::EPI_CPR;
         const int chunk = q ^ ((r / T::EPI_RPP) & (T::EPI_CPR - 1));
         u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * T::EPI_ROWB + chunk * 16);
-        if ((r >> 4) & 1)
+        if ((r >> T::EPI_HALF_BIT) & 1)
           v = (u32x4){v[2], v[3], v[0], v[1]};
         const int row = m0 + wm * T::WTM + r;
         const int col = n0 + wn * T::WTN + 8 * q;

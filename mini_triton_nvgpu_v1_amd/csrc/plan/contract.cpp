@@ -173,8 +173,14 @@ static void checkKernelSwizzle(const KernelContract &k) {
   int64_t aPP = std::max<int64_t>(1, 256 / (c.blockK * 2)), aMax = c.blockK / 8;
   int64_t bPP = std::max<int64_t>(1, 256 / (c.blockN * 2)),
           bMax = std::min<int64_t>(4, c.blockN / 32);
+  // the 16x16x32 instance's B reads add the second XOR term (32-byte units,
+  // phase (k / 8) % 2); the general loop has none
+  const bool m16 = c.mmaKind == MmaKind::Mfma16x16x32F16;
+  const int64_t b2pp = m16 ? 8 : 0, b2mp = m16 ? 2 : 0, b2w = m16 ? 32 : 0;
   if (a.perPhase != aPP || a.maxPhase != aMax || a.swizzlingByteWidth != 16 ||
-      b.perPhase != bPP || b.maxPhase != bMax || b.swizzlingByteWidth != 64)
+      a.secondMaxPhase > 1 || b.perPhase != bPP || b.maxPhase != bMax ||
+      b.swizzlingByteWidth != 64 || b.secondPerPhase != b2pp ||
+      b.secondMaxPhase != b2mp || b.secondSwizzlingByteWidth != b2w)
     throw Error("LDS encoding of the plan differs from the swizzle compiled into "
                 "the gfx950 kernels");
 }

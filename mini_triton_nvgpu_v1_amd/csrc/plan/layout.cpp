@@ -111,6 +111,12 @@ SharedSwizzle sharedSwizzle(const Attr &shared) {
   s.maxPhase = paramI64(shared, "maxPhase");
   s.transposed = paramBool(shared, "transposed");
   s.swizzlingByteWidth = paramI64(shared, "swizzlingByteWidth");
+  for (const auto &kv : shared.params)
+    if (kv.first == "secondPerPhase") {
+      s.secondPerPhase = paramI64(shared, "secondPerPhase");
+      s.secondMaxPhase = paramI64(shared, "secondMaxPhase");
+      s.secondSwizzlingByteWidth = paramI64(shared, "secondSwizzlingByteWidth");
+    }
   return s;
 }
 
@@ -194,12 +200,18 @@ EncodingPlan deriveEncodingPlan(const KernelConfig &c, const TargetInfo &t,
                                {"cga", cga}});
   };
   auto shared = [&](const SharedSwizzle &sw) {
-    return Dialect("shared", {{"order", IntList(sw.order)},
-                              {"perPhase", IntU(sw.perPhase)},
-                              {"maxPhase", IntU(sw.maxPhase)},
-                              {"transposed", Bool(sw.transposed)},
-                              {"swizzlingByteWidth", IntU(sw.swizzlingByteWidth)},
-                              {"cga", cga}});
+    Fields f = {{"order", IntList(sw.order)},
+                {"perPhase", IntU(sw.perPhase)},
+                {"maxPhase", IntU(sw.maxPhase)},
+                {"transposed", Bool(sw.transposed)},
+                {"swizzlingByteWidth", IntU(sw.swizzlingByteWidth)},
+                {"cga", cga}};
+    if (sw.secondMaxPhase > 1) {
+      f.push_back({"secondPerPhase", IntU(sw.secondPerPhase)});
+      f.push_back({"secondMaxPhase", IntU(sw.secondMaxPhase)});
+      f.push_back({"secondSwizzlingByteWidth", IntU(sw.secondSwizzlingByteWidth)});
+    }
+    return Dialect("shared", f);
   };
   auto dot = [&](int64_t idx) {
     return Dialect("dot_operand", {{"operandIndex", IntU(idx)},
@@ -210,7 +222,20 @@ EncodingPlan deriveEncodingPlan(const KernelConfig &c, const TargetInfo &t,
   p.aGlobal = add("a_global", blocked(c.blockK, {nw, 1}));
   p.bGlobal = add("b_global", blocked(c.blockN, {nw, 1}));
   p.aShared = add("a_shared", shared(deriveSwizzle(t, c.blockK * elem, 16)));
-  p.bShared = add("b_shared", shared(deriveSwizzle(t, c.blockN * elem, 64)));
+  // B's transposing reads: each 32-lane LDS cycle of a ds_read_b64_tr_b16
+  // serves two 16-lane groups, each reading 4 k rows of iN columns. With the
+  // 32x32 layout the two groups read the same rows, 16 columns apart: one
+  // 64-byte segment per row, which the first term spreads over the banks.
+  // With the 16x16 layout they read the same iN = 16 columns of rows iK/4 = 8
+  // apart, so rows with equal k % 4 collide; a second XOR term on iN-column
+  // (32-byte) units with phase (k / 8) % 2 separates the groups.
+  SharedSwizzle bSwizzle = deriveSwizzle(t, c.blockN * elem, 64);
+  if (iM == 16 && bSwizzle.maxPhase > 1 && iN * elem * 2 <= bSwizzle.swizzlingByteWidth) {
+    bSwizzle.secondPerPhase = iK / 4;
+    bSwizzle.secondMaxPhase = 2;
+    bSwizzle.secondSwizzlingByteWidth = iN * elem;
+  }
+  p.bShared = add("b_shared", shared(bSwizzle));
   p.aDot = add("a_dot", dot(0));
   p.bDot = add("b_dot", dot(1));
   p.acc = add("acc", Dialect("accumulator",

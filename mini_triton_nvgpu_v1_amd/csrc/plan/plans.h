@@ -212,6 +212,10 @@ struct SharedSwizzle {
   I64s order;
   int64_t perPhase = 1, maxPhase = 1, swizzlingByteWidth = 0;
   bool transposed = false;
+  // gfx950: a second XOR term, on units of secondSwizzlingByteWidth inside a
+  // first-term unit, phase (row / secondPerPhase) % secondMaxPhase
+  // (secondMaxPhase <= 1: none)
+  int64_t secondPerPhase = 0, secondMaxPhase = 0, secondSwizzlingByteWidth = 0;
 };
 SharedSwizzle sharedSwizzle(const Attr &shared);
 

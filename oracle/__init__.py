@@ -74,6 +74,8 @@ def lib() -> ctypes.CDLL:
         L.tbo_split_k_range.restype = None
         L.tbo_swizzle_minor.argtypes = [i64, i64, i64, i64, i64, i64]
         L.tbo_swizzle_minor.restype = i64
+        L.tbo_swizzle_minor2.argtypes = [i64] * 9
+        L.tbo_swizzle_minor2.restype = i64
         _lib = L
     return _lib
 
@@ -205,3 +207,11 @@ def swizzle_minor(major: int, minor: int, per_phase: int, max_phase: int,
                   span_elems: int, minor_extent: int) -> int:
     return lib().tbo_swizzle_minor(major, minor, per_phase, max_phase,
                                    span_elems, minor_extent)
+
+
+def swizzle_minor2(major: int, minor: int, per_phase: int, max_phase: int,
+                   span_elems: int, per_phase2: int, max_phase2: int,
+                   span2_elems: int, minor_extent: int) -> int:
+    """swizzle_minor, then the gfx950 second XOR term on span2 units."""
+    return lib().tbo_swizzle_minor2(major, minor, per_phase, max_phase, span_elems,
+                                    per_phase2, max_phase2, span2_elems, minor_extent)

@@ -395,3 +395,21 @@ int64_t tbo_swizzle_minor(int64_t major, int64_t minor, int64_t per_phase,
   int64_t chunk = minor / span_elems, in_chunk = minor % span_elems;
   return ((chunk ^ phase) % chunks) * span_elems + in_chunk;
 }
+
+/* The gfx950 shared encoding with a second XOR term: the reference's swizzle
+ * above, then the unit of span2_elems elements inside it XORed with
+ * (major / per_phase2) % max_phase2 (span2 * max_phase2 <= span, so the term
+ * permutes units inside one first-term span). max_phase2 <= 1 = no second
+ * term. */
+int64_t tbo_swizzle_minor2(int64_t major, int64_t minor, int64_t per_phase,
+                           int64_t max_phase, int64_t span_elems, int64_t per_phase2,
+                           int64_t max_phase2, int64_t span2_elems,
+                           int64_t minor_extent) {
+  int64_t m1 = tbo_swizzle_minor(major, minor, per_phase, max_phase, span_elems,
+                                 minor_extent);
+  if (max_phase2 <= 1 || span2_elems <= 0)
+    return m1;
+  int64_t pp2 = per_phase2 > 1 ? per_phase2 : 1;
+  int64_t phase2 = (major / pp2) % max_phase2;
+  return ((m1 / span2_elems) ^ phase2) * span2_elems + m1 % span2_elems;
+}

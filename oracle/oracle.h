@@ -83,6 +83,11 @@ void tbo_split_k_range(int64_t tiles_k, int64_t split_k, int64_t part,
 int64_t tbo_swizzle_minor(int64_t major, int64_t minor, int64_t per_phase,
                           int64_t max_phase, int64_t span_elems,
                           int64_t minor_extent);
+/* the same plus the gfx950 second XOR term on span2-element units */
+int64_t tbo_swizzle_minor2(int64_t major, int64_t minor, int64_t per_phase,
+                           int64_t max_phase, int64_t span_elems, int64_t per_phase2,
+                           int64_t max_phase2, int64_t span2_elems,
+                           int64_t minor_extent);
 
 #ifdef __cplusplus
 }

@@ -293,3 +293,59 @@ def test_swizzle_known_answer_and_bijection():
         perm = [oracle.swizzle_minor(row, c, 1, 8, 8, 64) for c in range(64)]
         assert sorted(perm) == list(range(64))
     assert oracle.swizzle_minor(5, 3, 1, 1, 8, 64) == 3  # maxPhase 1: identity
+
+
+def _bank_conflict_ways(addrs, bytes_per_lane, lanes_per_cycle):
+    """Brute-force LDS bank model of gfx950 (64 banks x 4 bytes): the lanes
+    of one cycle are served together; the cycle's cost is the largest number
+    of distinct 4-byte words any one bank must deliver."""
+    worst = 1
+    for c0 in range(0, len(addrs), lanes_per_cycle):
+        words = {}
+        for a in addrs[c0:c0 + lanes_per_cycle]:
+            for w in range(a // 4, (a + bytes_per_lane) // 4):
+                words.setdefault(w % 64, set()).add(w)
+        worst = max(worst, max(len(v) for v in words.values()))
+    return worst
+
+
+def _mfma16_b_read_addrs(second_term):
+    """Byte addresses of one ds_read_b64_tr_b16 of the 16x16x32 B fragment
+    (tile jj = 0, k step 0, first half) in a [64][256] f16 stage: lane l reads
+    k row 8 (l/16) + (l%16)/4, columns 4 (l%4) .. +3, through the plan's
+    swizzle (64-byte segments XOR k % 4; optionally 32-byte units XOR
+    (k / 8) % 2)."""
+    addrs = []
+    for lane in range(64):
+        k = 8 * (lane // 16) + (lane % 16) // 4
+        n = 4 * (lane % 4)
+        if second_term:
+            phys = oracle.swizzle_minor2(k, n, 1, 4, 32, 8, 2, 16, 256)
+        else:
+            phys = oracle.swizzle_minor(k, n, 1, 4, 32, 256)
+        addrs.append(k * 512 + phys * 2)
+    return addrs
+
+
+def test_second_swizzle_term_bijection_and_bank_conflicts():
+    """The gfx950 second XOR term keeps every row a permutation, reduces to
+    the reference's swizzle when off, and makes the 16x16x32 B read
+    conflict-free: without it the two 16-lane groups of a cycle (k rows 8
+    apart, same k % 4) hit the same banks, a 2-way conflict (what the
+    SQ_LDS_BANK_CONFLICT counter showed on the GPU)."""
+    for k in range(64):
+        perm = [oracle.swizzle_minor2(k, n, 1, 4, 32, 8, 2, 16, 256) for n in range(256)]
+        assert sorted(perm) == list(range(256))
+        # the second term moves whole 16-column (32-byte) units inside a
+        # 32-column (64-byte) segment of the first
+        for n in range(0, 256, 16):
+            assert perm[n] // 32 == oracle.swizzle_minor(k, n, 1, 4, 32, 256) // 32
+        assert [oracle.swizzle_minor2(k, n, 1, 4, 32, 8, 1, 16, 256) for n in range(256)] == \
+            [oracle.swizzle_minor(k, n, 1, 4, 32, 256) for n in range(256)]
+    # closed form of the encoding: chunk' = chunk ^ 4 (k % 4) ^ 2 ((k / 8) % 2)
+    for k in range(32):
+        for chunk in range(32):
+            got = oracle.swizzle_minor2(k, 8 * chunk, 1, 4, 32, 8, 2, 16, 256) // 8
+            assert got == chunk ^ (4 * (k % 4)) ^ (2 * ((k // 8) % 2))
+    assert _bank_conflict_ways(_mfma16_b_read_addrs(False), 8, 32) == 2
+    assert _bank_conflict_ways(_mfma16_b_read_addrs(True), 8, 32) == 1
