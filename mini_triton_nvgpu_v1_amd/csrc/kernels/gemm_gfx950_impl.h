@@ -3,6 +3,7 @@
 #pragma once
 
 #include "gemm_gfx950.h"
+#include "mfma16_schedule.h"
 
 #include <type_traits>
 #include <utility>
@@ -281,8 +282,11 @@ __device__ __forceinline__ void sched_step() {
 // information, so (a) each accumulator's first MFMA takes srcC = 0 (no
 // zeroing write right before it), (b) 24 wait states separate the last MFMA
 // from the first accumulator read, and (c) every fragment register is
-// rewritten at least 8 MFMA slots after its last MFMA read. LDS results are
-// waited for by the compiler's lgkmcnt tracking of the asm operands.
+// rewritten at least 8 MFMA slots after its last MFMA read. The slot
+// schedule and these rules are constexpr in Mfma16Schedule (mfma16_schedule.h)
+// and static_assert-ed there, so a schedule edit that breaks one does not
+// compile. LDS results are waited for by the compiler's lgkmcnt tracking of
+// the asm operands.
 //
 // Per 16x16x32 tile ii, jj (0..7) of the wave's 128x128: lane l holds
 // A[16ii + l%16][k0 + 8(l/16) .. +7] (one ds_read_b128) and
@@ -308,7 +312,10 @@ constexpr int kMfma16LgkmLoop = 0;
 
 template <bool EPI>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
-  constexpr int BK = 64, BQ = 40, LS = 5;
+  // slots, read placement and hazard rules: Mfma16Schedule (compile-time
+  // checked)
+  using Sched = Mfma16Schedule<>;
+  constexpr int BK = 64, BQ = Sched::BQ, LS = 5;
   constexpr uint32_t SLOT = 65536; // ring slot: A [256][64] at 0, B [64][256] at 32 KiB
   constexpr uint32_t B_AT = 32768;
   const int lane = threadIdx.x & 63;
@@ -388,12 +395,12 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // read op o (0..23) of k step ks into buffer buf: A0, B0 (halves 0, 1) ..
   // B7, A1 .. A7
   auto rd = [&](int buf, int st, int ks, int o) {
-    if (o == 0 || o >= 17) {
-      const int i = o == 0 ? 0 : o - 16;
+    if (Sched::op_is_a(o)) {
+      const int i = Sched::op_index(o);
       fa[buf][i] = __builtin_bit_cast(
           half8, *(const TBK_LDS u32x4 *)(uintptr_t)(a_base[st][ks] + i * 2048));
     } else {
-      const int j = (o - 1) >> 1, r = (o - 1) & 1;
+      const int j = Sched::op_index(o), r = (o - 1) & 1;
       const half4 h = __builtin_bit_cast(
           half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TBK_LDS short4 *)(uintptr_t)(
                      b_base[st][j] + ks * 16384 + r * 2048)));
@@ -427,7 +434,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       mfma(0, m, first);
       static_for<24>([&](auto o_c) {
         constexpr int o = decltype(o_c)::value;
-        if constexpr ((8 * o) / 3 == m)
+        if constexpr (Sched::slot_ks0(o) == m)
           rd(1, st, 1, o);
       });
       extra(m);
@@ -482,11 +489,14 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     static_assert(kMfma16VmLoop == 0 && kMfma16LgkmLoop == 0, "barrier wait below");
     wait_vmcnt_lgkm0<kMfma16VmLoop>();
     barrier();
-    static_assert(64 - BQ == 24, "one read op per slot after the barrier");
     static_for<64 - BQ>([&](auto s_c) {
       constexpr int m = BQ + decltype(s_c)::value;
       mfma(1, m, false);
-      rd(0, Sn, 0, m - BQ);
+      static_for<Sched::NREAD>([&](auto o_c) {
+        constexpr int o = decltype(o_c)::value;
+        if constexpr (Sched::slot_ks1(o) == m)
+          rd(0, Sn, 0, o);
+      });
       if constexpr (((m - BQ) % LS) == 0)
         load(ra, rb, it + 2, stage, (m - BQ) / LS);
       __builtin_amdgcn_sched_barrier(0);
@@ -509,7 +519,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   if (it < nk - 1)
     body(it, S0{});
   kstep1(Q{}, E{}); // the last k-tile after its barrier point
-  // 24 wait states between the last MFMA and the first accumulator read
+  // Sched::ACC_READ_WAITS (24) wait states between the last MFMA and the
+  // first accumulator read
+  static_assert(Sched::ACC_READ_WAITS == 24, "three s_nop 7 below");
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
   wait_vmcnt<0>(); // the zero loads past the end have landed too
 
