@@ -1104,8 +1104,12 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                 v[e] = epi_apply1(v[e], b[e], ea);
             }
           }
+          // f32 results (split-K partials, plain f32 C) are written once and
+          // not read again by this kernel: non-temporal, which leaves less
+          // dirty data in L2 for the kernel-end release (split-K 512^2 x
+          // 16384: 15.7 -> 15.1 us per GEMM); C += A*B keeps the default
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
-                                                 0, 0);
+                                                 0, OUT == kOutF32Partial ? kStoreNT : 0);
         }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {
