@@ -24,7 +24,8 @@
 
 namespace tbk {
 
-template <int BQ_ = 40, int RNUM = 8, int RDEN = 3, int ACC_WAITS = 24>
+template <int BQ_ = 16, int RNUM = 8, int RDEN = 3, int ACC_WAITS = 24, int R1NUM = 2,
+          int R1DEN = 1>
 struct Mfma16Schedule {
   static constexpr int NSLOT = 64;  // MFMAs per 32-deep k step: 8 x 8 tiles of 16 x 16
   static constexpr int NREAD = 24;  // fragment reads per k step: A0, B0 (2 halves) .. B7, A1 .. A7
@@ -42,7 +43,7 @@ struct Mfma16Schedule {
   // slot of read op o: in k step 0, the reads of k step 1 (fragment buffer 1);
   // in k step 1 after the barrier, the next k-tile's k step 0 (buffer 0)
   static constexpr int slot_ks0(int o) { return RNUM * o / RDEN; }
-  static constexpr int slot_ks1(int o) { return BQ + o; }
+  static constexpr int slot_ks1(int o) { return BQ + R1NUM * o / R1DEN; }
 
   static constexpr int last_read(bool a, int idx) {
     int last = -1;
@@ -96,7 +97,7 @@ struct Mfma16Schedule {
   static_assert(covers_every_tile_once(), "(a) first-MFMA srcC = 0 needs one MFMA per tile");
   static_assert(reads_fit(), "fragment reads must fall inside their k step (and after the "
                              "barrier for the next k-tile's reads)");
-  static_assert(BQ + NREAD <= NSLOT, "the next k-tile's reads must fit after the barrier");
+  static_assert(slot_ks1(NREAD - 1) < NSLOT, "the next k-tile's reads must fit after the barrier");
   static_assert(min_rewrite_distance() >= MIN_REWRITE_SLOTS,
                 "(c) a fragment register rewritten too soon after its last MFMA read");
   static_assert(ACC_READ_WAITS >= 3 * PASSES && ACC_READ_WAITS % 8 == 0,

@@ -28,20 +28,24 @@ def _compile(tmp_path, params):
 def test_kernel_schedule_builds(tmp_path):
     p = _compile(tmp_path, "")  # the defaults the kernel instantiates
     assert p.returncode == 0, p.stderr
-    p = _compile(tmp_path, "40, 8, 3, 24")
+    p = _compile(tmp_path, "16, 8, 3, 24, 2, 1")
+    assert p.returncode == 0, p.stderr
+    # the earlier schedule (barrier at slot 40, one read per slot after it)
+    # keeps the rules too
+    p = _compile(tmp_path, "40, 8, 3, 24, 1, 1")
     assert p.returncode == 0, p.stderr
 
 
 @pytest.mark.parametrize("params,rule", [
     # (b) two s_nop 7 instead of three
-    ("40, 8, 3, 16", "(b) accumulator reads need 3 wait states per MFMA pass"),
+    ("16, 8, 3, 16, 2, 1", "(b) accumulator reads need 3 wait states per MFMA pass"),
     # (c) k step 1's reads bunched at the start of k step 0: A7's buffer-1
     # register rewritten 6 slots after the previous k step's last read of it
-    ("40, 1, 4, 24", "(c) a fragment register rewritten too soon"),
+    ("16, 1, 4, 24, 2, 1", "(c) a fragment register rewritten too soon"),
     # the next k-tile's reads would run past the k step
-    ("48, 8, 3, 24", "the next k-tile's reads must fit after the barrier"),
+    ("24, 8, 3, 24, 2, 1", "the next k-tile's reads must fit after the barrier"),
     # k step 1's reads spread past the end of k step 0
-    ("40, 3, 1, 24", "fragment reads must fall inside their k step"),
+    ("16, 3, 1, 24, 2, 1", "fragment reads must fall inside their k step"),
 ])
 def test_schedule_edits_that_break_a_rule_do_not_build(tmp_path, params, rule):
     p = _compile(tmp_path, params)
