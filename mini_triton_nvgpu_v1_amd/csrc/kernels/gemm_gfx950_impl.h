@@ -253,9 +253,10 @@ __device__ __forceinline__ void sched_step() {
 }
 
 // ---- 4 waves of 128x128 on a 256x256x64 tile with v_mfma_f32_16x16x32_f16 ------
-// The instance the plan selects for whole tiles of the 4-wave 256x256x64
-// 2-stage f16 configuration (mma = mfma_f32_16x16x32_f16): one wave per
-// SIMD, M and N multiples of 256, K of 64, tile / grouped / persistent order.
+// The instance the plan selects for the 4-wave 256x256x64 2-stage f16
+// configuration (mma = mfma_f32_16x16x32_f16): one wave per SIMD, any M and
+// N (ragged edges masked at the loads and the C store), K a multiple of 64,
+// tile / grouped / persistent order.
 // It fills the same LDS ring with the same swizzles as the general loop.
 //
 // Why 16x16x32: per FLOP it reads and writes a quarter of the accumulator
@@ -269,8 +270,10 @@ __device__ __forceinline__ void sched_step() {
 //    scalar offsets per load round, per-stage LDS bases; the k step, row
 //    group and B half ride in the ds_read immediate offset, and M0 is formed
 //    with an immediate add inside the load asm (no SGPR per stage and round);
-//  * no per-load bounds checks: tiles are whole, and the ring's lookahead
-//    loads past the last k-tile use a descriptor of zero records (zeros);
+//  * no per-load address arithmetic for bounds: a lane's A row validity is a
+//    compare against a constant per round, its B column validity is fixed,
+//    and the ring's lookahead loads past the last k-tile use a descriptor of
+//    zero records (zeros);
 //  * one loop iteration runs from a k-tile's barrier to the next, so the
 //    compiler's waits for fragment reads never land in front of the first
 //    MFMAs of a k-tile; the barrier is vmcnt(0) lgkmcnt(0) + s_barrier (this
@@ -333,15 +336,28 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // every 16 k rows, i.e. every 2 rounds, so a lane fetches one logical
   // chunk in every A round and one per round parity in B; only the scalar
   // offset moves.
+  // Ragged M and N (K is a multiple of 64): A round l covers rows
+  // m0 + a_row0 + 32l and is loaded only while that row is below M; B columns
+  // at or past N load from kOob. The buffer range check covers the vector
+  // offset only, not the scalar offset that carries the round and the
+  // k-tile, so a row past M is refused here rather than left to the check.
+  // Past the edge the ring holds zeros, which only reach C elements outside
+  // M x N, and those are not stored.
   const int a_row0 = (wave * 64 + lane) >> 3;
   const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
-  const uint32_t a_voff = ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + a_lc * 8) * 2u;
+  const int a_rows_left = p.M - m0 - a_row0;
+  const uint32_t a_voff =
+      a_rows_left > 0 ? ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + a_lc * 8) * 2u : kOob;
   const int b_row0 = (wave * 64 + lane) >> 5; // 0 .. 7: (k / 8) % 2 = round % 2
   const int b_lc = (lane & 31) ^ (4 * (b_row0 & 3));
   const uint32_t b_voff0 =
-      ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + b_lc * 8)) * 2u;
+      n0 + b_lc * 8 < p.N
+          ? ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + b_lc * 8)) * 2u
+          : kOob;
   const uint32_t b_voff1 =
-      ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + (b_lc ^ 2) * 8)) * 2u;
+      n0 + (b_lc ^ 2) * 8 < p.N
+          ? ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + (b_lc ^ 2) * 8)) * 2u
+          : kOob;
   const uint32_t a_round = 32u * (uint32_t)p.lda * 2u, b_round = 8u * (uint32_t)p.ldb * 2u;
   const uint32_t a_ktile = BK * 2u, b_ktile = BK * 2u * (uint32_t)p.ldb;
   const uint32_t a_bytes = (uint32_t)p.M * (uint32_t)p.lda * 2u;
@@ -355,7 +371,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       constexpr int L = decltype(l_c)::value;
       if (L == l) {
         if constexpr (L < 8)
-          load_lds16_at<base + L * 4096u>(ra, wlds, a_voff,
+          load_lds16_at<base + L * 4096u>(ra, wlds, L * 32 < a_rows_left ? a_voff : kOob,
                                           (uint32_t)kt * a_ktile + L * a_round);
         else
           load_lds16_at<base + B_AT + (L - 8) * 4096u>(rb, wlds, (L & 1) ? b_voff1 : b_voff0,
@@ -594,8 +610,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     u32x4 v = *(const TBK_LDS u32x4 *)(wl + r * 256 + ((q ^ (r & 7)) * 16));
     if ((r >> 3) & 1)
       v = (u32x4){v[2], v[3], v[0], v[1]};
-    const uint32_t off = ((uint32_t)(m0 + wm * 128 + r) * (uint32_t)p.ldc +
-                          (uint32_t)(n0 + wn * 128 + 8 * q)) * 2u;
+    const int row = m0 + wm * 128 + r, col = n0 + wn * 128 + 8 * q;
+    const uint32_t off = row < p.M && col < p.N
+                             ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u
+                             : kOob;
     // non-temporal (nt): C is written once and not read again by this
     // kernel; measured 0.7% faster at 4096^3 than the default policy
     __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
@@ -1196,7 +1214,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 }
 
 // The 16x16x32 instance of the 4-wave 256x256x64 2-stage f16 configuration
-// (whole tiles; tile, grouped or persistent order).
+// (any M and N, K a multiple of 64; tile, grouped or persistent order).
 template <bool EPI>
 __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
   __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves

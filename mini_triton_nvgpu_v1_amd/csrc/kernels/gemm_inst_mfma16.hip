@@ -1,5 +1,6 @@
 // The v_mfma_f32_16x16x32_f16 instances of the 4-wave 256x256x64 2-stage
-// f16 tile (whole tiles; tile, grouped or persistent order), plain and with
+// f16 tile (any M and N, K a multiple of 64; tile, grouped or persistent
+// order), plain and with
 // the fused epilogue steps.
 #include "gemm_gfx950_impl.h"
 

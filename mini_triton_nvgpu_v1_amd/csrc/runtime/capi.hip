@@ -95,11 +95,9 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
     return fail("group_m must be >= 1");
   if (c.mfma != TB_MFMA_32X32X16 && c.mfma != TB_MFMA_16X16X32)
     return fail("mfma must be TB_MFMA_32X32X16 or TB_MFMA_16X16X32");
-  if (c.mfma == TB_MFMA_16X16X32 &&
-      (c.m % c.block_m || c.n % c.block_n || c.k % c.block_k ||
-       c.mapping == TB_MAP_SPLIT_K))
-    return fail("the 16x16x32 instance runs whole tiles only (M, N multiples of "
-                "block_m, block_n, K of block_k) and no split-K");
+  if (c.mfma == TB_MFMA_16X16X32 && (c.k % c.block_k || c.mapping == TB_MAP_SPLIT_K))
+    return fail("the 16x16x32 instance runs whole k-tiles only (K a multiple of "
+                "block_k) and no split-K");
   const int64_t tiles_m = ceil_div(c.m, c.block_m);
   const int64_t tiles_n = ceil_div(c.n, c.block_n);
   const int64_t tiles_k = ceil_div(c.k, c.block_k);

@@ -77,8 +77,7 @@ def test_mfma_16x16x32_instance_selection():
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(mfma=2), "TB_MFMA_"),
-    (dict(m=4096 - 8), "whole tiles"),
-    (dict(k=4096 - 32, lda=4096 - 32), "whole tiles"),
+    (dict(k=4096 - 32, lda=4096 - 32), "whole k-tiles"),
     (dict(stages=3), "no gfx950 kernel instance.*16x16x32"),
     (dict(c_dtype=tb.DTYPE_F32), "no gfx950 kernel instance.*16x16x32"),
 ])

@@ -1,13 +1,16 @@
 """GPU parity of the 16x16x32 instance of the 4-wave 256x256x64 tile.
 
-`256x256x64_w2x2_s2_out0_16x16x32[_epi]` runs whole tiles (M and N multiples
-of 256, K of 64; tile, grouped or persistent order) with one wave per SIMD,
-128x128 wave tiles and v_mfma_f32_16x16x32_f16, on the same LDS ring as the
-general loop. Checks:
+`256x256x64_w2x2_s2_out0_16x16x32[_epi]` runs any M and N with K a multiple
+of 64 (tile, grouped or persistent order) with one wave per SIMD, 128x128
+wave tiles and v_mfma_f32_16x16x32_f16, on the same LDS ring as the general
+loop; ragged edges are masked at the A and B loads and at the C store.
+Checks:
 
 * against the fp64 oracle, |got - ref| <= 1e-2 * (|ref| + 1), on shapes that
   cover 1, 2, odd and even k-tile counts, tile / grouped / persistent orders
-  (more tiles than programs), padded leading dimensions and the fused steps;
+  (more tiles than programs), padded leading dimensions, ragged M and N
+  (including a problem smaller than one wave tile, and padding columns that
+  must stay unwritten) and the fused steps;
 * bit-identity with the general loop at 8 waves (`w4x2`) and at 4 waves
   (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
   products in the same k order (in 32x32x16 or 16x16x32 steps), and the
@@ -17,8 +20,8 @@ general loop. Checks:
   instance and the general loop's fused instance, and the fused instance in
   persistent order.
 
-Ragged shapes take the general loop (test_gemm_gpu.py: test_ragged_edges,
-test_every_instance).
+K not a multiple of 64 takes the general loop (test_gemm_gpu.py:
+test_ragged_edges, test_every_instance).
 """
 import numpy as np
 import pytest
@@ -33,7 +36,7 @@ RTOL = 1e-2
 
 def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0, mfma16=False):
     wgm, wgn = (2, 2) if waves == 4 else (4, 2)
-    tm, tn = M // 256, N // 256
+    tm, tn = -(-M // 256), -(-N // 256)
     return tb.GemmConfig(
         m=M, n=N, k=K, lda=K + ld_pad, ldb=N + ld_pad, ldc=N + ld_pad,
         c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, block_m=256, block_n=256,
@@ -66,6 +69,11 @@ CASES = [
     (1024, 1024, 128, tb.MAP_PERSISTENT_GROUPED, 3, 0, 0),  # 16 tiles on 3 programs
     (768, 1024, 64, tb.MAP_PERSISTENT_TILE, 5, 0, 0),    # 12 tiles on 5 programs
     (2048, 2048, 128, tb.MAP_GROUPED_TILE, None, 0, 8),  # 64 tiles, XCD order
+    (300, 520, 192, tb.MAP_GROUPED_TILE, None, 0, 0),    # ragged M and N
+    (100, 72, 128, tb.MAP_TILE, None, 0, 0),             # smaller than a wave tile
+    (1000, 1496, 768, tb.MAP_GROUPED_TILE, None, 8, 0),  # ragged, padding untouched
+    (1300, 904, 512, tb.MAP_PERSISTENT_GROUPED, 7, 0, 0),  # 24 ragged tiles on 7
+    (2000, 2056, 256, tb.MAP_GROUPED_TILE, None, 0, 8),  # 72 ragged tiles, XCD order
 ]
 
 
@@ -79,6 +87,8 @@ def test_mfma16_matches_oracle_and_general_loop(M, N, K, mapping, programs, pad,
     name16, got16 = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd, mfma16=True),
                          A, B, device, pad)
     assert name16 == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
+    if pad:  # columns past N stay as they were (NaN)
+        assert np.isnan(got16[:, N:].astype(np.float32)).all()
     got16 = got16[:, :N]
     ref = oracle.gemm_f64(A, B)
     bad, err, worst = oracle.check_tolerance(got16, ref, rtol=RTOL)
