@@ -168,10 +168,9 @@ class Workload:
 
     def mfma16_supported(self) -> bool:
         """The plan's choice of v_mfma_f32_16x16x32_f16: the 4-wave
-        256x256x64 2-stage f16 tile, any M and N, K a multiple of 64, no
-        split-K."""
+        256x256x64 2-stage f16 tile, any M, N and K, no split-K."""
         return (self.block == (256, 256, 64) and self.num_waves == 4 and self.stages == 2
-                and self.K % 64 == 0 and self.split_k == 1)
+                and self.split_k == 1)
 
 
 SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,
@@ -181,7 +180,7 @@ RAGGED = Workload("ragged_96x80x32", 96, 80, 32, 0x5EED0002, UNIFORM,
 RAGGED_128 = Workload("tile_128x128x32", 128, 128, 32, 0x5EED0003, UNIFORM,
                       (128, 128, 32), num_waves=4)
 # 4 waves of 128x128 (one per SIMD) on the 256x256 tile: a third fewer LDS
-# fragment bytes per MFMA than 8 waves of 64x128, and (K a multiple of 64) the
+# fragment bytes per MFMA than 8 waves of 64x128, and the
 # 16x16x32 instance, a quarter of the accumulator register traffic per FLOP:
 # less energy per launch, a higher sustained clock on this power-limited part
 # (~14% faster than 8 waves of 32x32x16)

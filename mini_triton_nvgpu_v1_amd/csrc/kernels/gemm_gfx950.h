@@ -202,6 +202,10 @@ struct KernelEntry {
   // wait, vmcnt at the per-k-tile barrier, lgkmcnt at that barrier (-1: none;
   // the compiler orders the LDS reads). The plan's AsyncPlan must state them.
   int vm_prologue, vm_loop, lgkm_loop;
+  // the same instance built for a partial last k-tile (K % block_k != 0),
+  // where its whole-K build carries no masking: the launcher picks it then
+  // (null: fn handles every K)
+  const void *fn_partial_k;
 };
 
 // Registry of compiled instances (defined in the instance files).

@@ -254,9 +254,9 @@ __device__ __forceinline__ void sched_step() {
 
 // ---- 4 waves of 128x128 on a 256x256x64 tile with v_mfma_f32_16x16x32_f16 ------
 // The instance the plan selects for the 4-wave 256x256x64 2-stage f16
-// configuration (mma = mfma_f32_16x16x32_f16): one wave per SIMD, any M and
-// N (ragged edges masked at the loads and the C store), K a multiple of 64,
-// tile / grouped / persistent order.
+// configuration (mma = mfma_f32_16x16x32_f16): one wave per SIMD, any M, N
+// and K (ragged edges masked at the loads and the C store), tile / grouped /
+// persistent order.
 // It fills the same LDS ring with the same swizzles as the general loop.
 //
 // Why 16x16x32: per FLOP it reads and writes a quarter of the accumulator
@@ -314,7 +314,7 @@ constexpr int kMfma16VmPrologue = kMfma16LoadsPerThread;
 constexpr int kMfma16VmLoop = 0;
 constexpr int kMfma16LgkmLoop = 0;
 
-template <bool EPI>
+template <bool EPI, bool KPART>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
   // slots, read placement and hazard rules: Mfma16Schedule (compile-time
   // checked)
@@ -326,7 +326,11 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(TBK_LDS void *)lds;
-  const int nk = p.K / BK;
+  // KPART: the build for K % 64 != 0 (the last k-tile is partial); the
+  // launcher takes it only then, so the whole-K build carries none of its
+  // masking code
+  const int nk = (p.K + BK - 1) / BK; // k-tiles
+  const int kfull = p.K / BK;          // whole k-tiles
 
   // Direct loads: round l of wave w fills 1 KiB at slot + l * 4 KiB + w * 1 KiB
   // (A rows 32l + 8w .. +7; B k-rows 8l + 2w, +1). B's 16-byte chunk c of
@@ -336,13 +340,16 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // every 16 k rows, i.e. every 2 rounds, so a lane fetches one logical
   // chunk in every A round and one per round parity in B; only the scalar
   // offset moves.
-  // Ragged M and N (K is a multiple of 64): A round l covers rows
-  // m0 + a_row0 + 32l and is loaded only while that row is below M; B columns
-  // at or past N load from kOob. The buffer range check covers the vector
-  // offset only, not the scalar offset that carries the round and the
-  // k-tile, so a row past M is refused here rather than left to the check.
-  // Past the edge the ring holds zeros, which only reach C elements outside
-  // M x N, and those are not stored.
+  // Ragged edges. A round l covers rows m0 + a_row0 + 32l and is loaded only
+  // while that row is below M; B columns at or past N load from kOob. In a
+  // partial last k-tile (K % 64 = 8r, r = 1..7) a lane's A chunk holds
+  // k = 64 kfull + 8 a_lc and loads from kOob unless a_lc < r, and B round l
+  // holds k rows 64 kfull + 8l .. +7, so rounds l >= r take a descriptor of
+  // zero records. The buffer range check covers the vector offset only, not
+  // the scalar offset that carries the round and the k-tile, so every such
+  // element is refused here rather than left to the check. Past the edges the
+  // ring holds zeros: in M and N they only reach C elements that are not
+  // stored, in K they add nothing.
   const int a_row0 = (wave * 64 + lane) >> 3;
   const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
   const int a_rows_left = p.M - m0 - a_row0;
@@ -363,23 +370,33 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const uint32_t a_bytes = (uint32_t)p.M * (uint32_t)p.lda * 2u;
   const uint32_t b_bytes = (uint32_t)p.K * (uint32_t)p.ldb * 2u;
   const uint32_t wlds = lds0 + wave * 1024u;
+  const int k_rounds = (p.K - kfull * BK) / 8; // B rounds of the partial k-tile
+  const uint32_t a_kmask = a_lc < k_rounds ? 0u : kOob;
+  const u32x4 rb_none = rsrc_dwords(p.B, 0u);
   // load l of k-tile kt into ring slot ST (l is a constant once unrolled:
-  // the LDS offset becomes the literal of the M0 add)
-  auto load = [&](const u32x4 &ra, const u32x4 &rb, int kt, auto st_c, int l) {
+  // the LDS offset becomes the literal of the M0 add). KMASK: kt may be the
+  // partial k-tile (the loop's whole-tile refills skip the masking code).
+  auto load = [&](const u32x4 &ra, const u32x4 &rb, int kt, auto st_c, int l,
+                  auto kmask_c) {
     constexpr uint32_t base = decltype(st_c)::value * SLOT;
+    constexpr bool KMASK = KPART && decltype(kmask_c)::value;
+    const bool kpart = KMASK && kt == kfull; // the partial k-tile (or past the end)
     static_for<16>([&](auto l_c) {
       constexpr int L = decltype(l_c)::value;
       if (L == l) {
         if constexpr (L < 8)
-          load_lds16_at<base + L * 4096u>(ra, wlds, L * 32 < a_rows_left ? a_voff : kOob,
-                                          (uint32_t)kt * a_ktile + L * a_round);
+          load_lds16_at<base + L * 4096u>(
+              ra, wlds, (L * 32 < a_rows_left ? a_voff : kOob) | (kpart ? a_kmask : 0u),
+              (uint32_t)kt * a_ktile + L * a_round);
         else
-          load_lds16_at<base + B_AT + (L - 8) * 4096u>(rb, wlds, (L & 1) ? b_voff1 : b_voff0,
-                                                       (uint32_t)kt * b_ktile +
-                                                           (L - 8) * b_round);
+          load_lds16_at<base + B_AT + (L - 8) * 4096u>(
+              kpart && L - 8 >= k_rounds ? rb_none : rb, wlds, (L & 1) ? b_voff1 : b_voff0,
+              (uint32_t)kt * b_ktile + (L - 8) * b_round);
       }
     });
   };
+  using KM = std::integral_constant<bool, true>;
+  using KW = std::integral_constant<bool, false>;
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
 
@@ -480,10 +497,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     const u32x4 rb1 = rsrc_dwords(p.B, nk > 1 ? b_bytes : 0u);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
-      load(ra, rb, 0, S0{}, l);
+      load(ra, rb, 0, S0{}, l, KM{});
 #pragma unroll
     for (int l = 0; l < 16; ++l)
-      load(ra1, rb1, 1, S1{}, l);
+      load(ra1, rb1, 1, S1{}, l, KM{});
   }
   wait_vmcnt<kMfma16VmPrologue>();
   barrier();
@@ -494,8 +511,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   kstep1(Z{}, Q{});
 
   // body(it): k-tile it (stage S) from its barrier on, k-tile it+1 (stage
-  // S^1) up to its barrier; stage S is refilled with k-tile it+2.
-  auto body = [&](int it, auto stage) {
+  // S^1) up to its barrier; stage S is refilled with k-tile it+2 (KMASK: the
+  // refill may be the partial k-tile).
+  auto body = [&](int it, auto stage, auto kmask_c) {
     constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(p.A, ok ? a_bytes : 0u);
@@ -515,7 +533,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
           rd(0, Sn, 0, o);
       });
       if constexpr (((m - BQ) % LS) == 0)
-        load(ra, rb, it + 2, stage, (m - BQ) / LS);
+        load(ra, rb, it + 2, stage, (m - BQ) / LS, kmask_c);
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int NB = (64 - BQ + LS - 1) / LS; // refill loads issued before k-tile it+1
@@ -523,18 +541,23 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     static_assert(OFF + (16 - NB - 1) * LS < 64, "refill fits one k-tile");
     auto refill = [&](int m) {
       if (m >= OFF && ((m - OFF) % LS) == 0 && NB + (m - OFF) / LS < 16)
-        load(ra, rb, it + 2, stage, NB + (m - OFF) / LS);
+        load(ra, rb, it + 2, stage, NB + (m - OFF) / LS, kmask_c);
     };
     kstep0(Sn, refill, false);
     kstep1(Z{}, Q{});
   };
   int it = 0;
+  if constexpr (KPART)
+    for (; it + 3 < kfull; it += 2) { // both refills are whole k-tiles
+      body(it, S0{}, KW{});
+      body(it + 1, S1{}, KW{});
+    }
   for (; it + 2 <= nk - 1; it += 2) {
-    body(it, S0{});
-    body(it + 1, S1{});
+    body(it, S0{}, KM{});
+    body(it + 1, S1{}, KM{});
   }
   if (it < nk - 1)
-    body(it, S0{});
+    body(it, S0{}, KM{});
   kstep1(Q{}, E{}); // the last k-tile after its barrier point
   // Sched::ACC_READ_WAITS (24) wait states between the last MFMA and the
   // first accumulator read
@@ -1220,8 +1243,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 }
 
 // The 16x16x32 instance of the 4-wave 256x256x64 2-stage f16 configuration
-// (any M and N, K a multiple of 64; tile, grouped or persistent order).
-template <bool EPI>
+// (any M, N and K; tile, grouped or persistent order).
+template <bool EPI, bool KPART>
 __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
   __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
   const bool persistent =
@@ -1236,7 +1259,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
     map_program(p, work, tile_m, tile_n, part);
     if (work != prog)
       __syncthreads(); // every wave read its staged epilogue back
-    mfma16_tile<EPI>(p, tile_m * 256, tile_n * 256, lds);
+    mfma16_tile<EPI, KPART>(p, tile_m * 256, tile_n * 256, lds);
   }
 }
 

@@ -95,9 +95,8 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
     return fail("group_m must be >= 1");
   if (c.mfma != TB_MFMA_32X32X16 && c.mfma != TB_MFMA_16X16X32)
     return fail("mfma must be TB_MFMA_32X32X16 or TB_MFMA_16X16X32");
-  if (c.mfma == TB_MFMA_16X16X32 && (c.k % c.block_k || c.mapping == TB_MAP_SPLIT_K))
-    return fail("the 16x16x32 instance runs whole k-tiles only (K a multiple of "
-                "block_k) and no split-K");
+  if (c.mfma == TB_MFMA_16X16X32 && c.mapping == TB_MAP_SPLIT_K)
+    return fail("the 16x16x32 instance has no split-K");
   const int64_t tiles_m = ceil_div(c.m, c.block_m);
   const int64_t tiles_n = ceil_div(c.n, c.block_n);
   const int64_t tiles_k = ceil_div(c.k, c.block_k);
@@ -288,7 +287,9 @@ static int launch_impl(const tb_gemm_desc *d, const void *a, const void *b, void
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   void *args[] = {&p};
   const dim3 grid((unsigned)cf.num_programs), block((unsigned)(cf.num_waves * 64));
-  if (int rc = check_hip(hipLaunchKernel(d->entry->fn, grid, block, args, 0, s),
+  const void *fn = d->entry->fn_partial_k && cf.k % cf.block_k ? d->entry->fn_partial_k
+                                                               : d->entry->fn;
+  if (int rc = check_hip(hipLaunchKernel(fn, grid, block, args, 0, s),
                          "hipLaunchKernel(gemm)"))
     return rc;
   if (cf.mapping == TB_MAP_SPLIT_K && cf.reduction == TB_RED_WORKSPACE) {

@@ -77,7 +77,8 @@ def test_mfma_16x16x32_instance_selection():
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(mfma=2), "TB_MFMA_"),
-    (dict(k=4096 - 32, lda=4096 - 32), "whole k-tiles"),
+    (dict(mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_WORKSPACE,
+          num_programs=512), "no split-K"),
     (dict(stages=3), "no gfx950 kernel instance.*16x16x32"),
     (dict(c_dtype=tb.DTYPE_F32), "no gfx950 kernel instance.*16x16x32"),
 ])

@@ -167,7 +167,7 @@ LARGE_RAGGED = [
     configs.Workload("ragged_persistent_1300x904x520", 1300, 904, 520, 0x5EED0202,
                      configs.NORMAL, (256, 256, 64), num_waves=4, persistent=True,
                      num_ctas=7, exact_tile=False),
-    # K a multiple of 64: the 16x16x32 instance on ragged M and N
+    # K a multiple of 64 (the ragged-K cases above take the same instance)
     configs.Workload("ragged16_1000x1496x768", 1000, 1496, 768, 0x5EED0203, configs.NORMAL,
                      (256, 256, 64), num_waves=4, exact_tile=False),
     configs.Workload("ragged16_persistent_1300x904x512", 1300, 904, 512, 0x5EED0204,
@@ -183,8 +183,8 @@ def test_large_ragged_parity(w, device):
     print(f"large ragged {w.name}", flush=True)
     A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
     desc = tb.plan_from_mlir(w.mlir())
-    # the 16x16x32 instance takes the 256x256x64 4-wave tiles whenever K is a
-    # multiple of 64, ragged M and N included
+    # the 16x16x32 instance takes the 256x256x64 4-wave tiles, ragged M, N
+    # and K included
     assert ("16x16x32" in desc.kernel_name) == w.mfma16_supported(), desc.kernel_name
     got = run_desc(desc, A, B, device)
     check(got, A, B)
@@ -241,12 +241,9 @@ EPI_STEPS = {0: (tb.EPI_BIAS_F16, tb.ACT_GELU_TANH, 3, -0.5, 1.5),
 def test_every_instance(inst, device):
     """Each compiled instance on a shape with several K tiles (more than the
     stage count, plus a ragged last tile when possible) and an M/N edge; the
-    16x16x32 instance (K a multiple of 64) on the same ragged M and N and 5
-    k-tiles."""
+    16x16x32 instance on the same shape."""
     bm, bn, bk, wgm, wgn, stages, out, epi, mfma16 = inst
     M, N, K = bm + 40, bn * 2 - 24, bk * 5 + (bk // 2 if out == 0 else 0)
-    if mfma16:
-        K = 5 * bk
     print(f"instance {inst} on {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0200 + bm + bn + bk, oracle.UNIFORM)
     tm, tn = -(-M // bm), -(-N // bn)

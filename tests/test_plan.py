@@ -192,16 +192,15 @@ def test_plan_from_mlir_diagnostics(name, text, arg, msg):
 
 def test_mfma_instruction_choice():
     """Without an `mma` attribute the plan takes 16x16x32 exactly where that
-    instance exists: the 4-wave 256x256x64 2-stage f16 tile with K a
-    multiple of 64 (M and N may be ragged) and without split-K. The EncodingPlan records the instruction shape."""
+    instance exists: the 4-wave 256x256x64 2-stage f16 tile (M, N and K may
+    be ragged) without split-K. The EncodingPlan records the instruction shape."""
     def launch(text):
         return tb.plan_from_mlir(text)
     wide = dict(M=512, N=768, K=192, bm=256, bn=256, bk=64)
     assert launch(matmul_module(**wide)).config.mfma == tb.MFMA_16X16X32
-    assert launch(matmul_module(**dict(wide, M=520, N=200, exact=False))).config.mfma == \
-        tb.MFMA_16X16X32
+    for kw in (dict(wide, M=520, N=200, exact=False), dict(wide, K=200, exact=False)):
+        assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_16X16X32, kw
     for kw in (dict(wide, warps=8), dict(wide, bk=32), dict(wide, c="f32"),
-               dict(wide, K=200, exact=False),
                dict(wide, extra_module=', "tb.split-k" = 3 : i64'),
                dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"'), {}):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_32X32X16, kw

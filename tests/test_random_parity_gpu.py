@@ -4,10 +4,9 @@ fused-step (`_epi`) instances and the split-K reduction's fused steps, each
 against the fp64 oracle (|got - ref| <= 1e-2 * (|ref| + 1)).
 
 A case draws an instance, a shape (M any size, N and K multiples of 8, the C
-ABI's transport rule; K a multiple of 64 for the 16x16x32 instance), GROUP_M, the
-XCD order and, per output mode, the mapping and program count (persistent
-orders get 1 .. tiles programs) or the split count (2 .. 8 with a
-workspace, 2 .. 6 atomic). The seed is fixed, so a failure reproduces; its
+ABI's transport rule), GROUP_M, the XCD order and, per output mode, the
+mapping and program count (persistent orders get 1 .. tiles programs) or the
+split count (2 .. 8 with a workspace, 2 .. 6 atomic). The seed is fixed, so a failure reproduces; its
 case line is printed before the launch.
 """
 import random
@@ -30,7 +29,7 @@ MAPS = [tb.MAP_TILE, tb.MAP_GROUPED_TILE, tb.MAP_PERSISTENT_TILE, tb.MAP_PERSIST
 def _case(rng, insts, case):
     bm, bn, bk, wgm, wgn, stages, out, _epi, mfma16 = rng.choice(insts)
     if mfma16:
-        M, N, K = rng.randint(1, 800), 8 * rng.randint(1, 100), 64 * rng.randint(1, 12)
+        M, N, K = rng.randint(1, 800), 8 * rng.randint(1, 100), 8 * rng.randint(1, 100)
     else:
         M, N, K = rng.randint(1, 600), 8 * rng.randint(1, 80), 8 * rng.randint(1, 128)
     tm, tn = -(-M // bm), -(-N // bn)
@@ -92,7 +91,7 @@ def _fused_case(rng, insts, case):
     f32 C, f32 C += A*B, or split-K (the steps then run in the reduction)."""
     bm, bn, bk, wgm, wgn, stages, out, _epi, mfma16 = rng.choice(insts)
     if mfma16:
-        M, N, K = rng.randint(1, 600), 8 * rng.randint(1, 90), 64 * rng.randint(1, 8)
+        M, N, K = rng.randint(1, 600), 8 * rng.randint(1, 90), 8 * rng.randint(1, 64)
     else:
         M, N, K = rng.randint(1, 400), 8 * rng.randint(1, 64), 8 * rng.randint(1, 96)
     tm, tn = -(-M // bm), -(-N // bn)

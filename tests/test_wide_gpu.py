@@ -1,16 +1,17 @@
 """GPU parity of the 16x16x32 instance of the 4-wave 256x256x64 tile.
 
-`256x256x64_w2x2_s2_out0_16x16x32[_epi]` runs any M and N with K a multiple
-of 64 (tile, grouped or persistent order) with one wave per SIMD, 128x128
-wave tiles and v_mfma_f32_16x16x32_f16, on the same LDS ring as the general
-loop; ragged edges are masked at the A and B loads and at the C store.
+`256x256x64_w2x2_s2_out0_16x16x32[_epi]` runs any M, N and K (tile, grouped
+or persistent order) with one wave per SIMD, 128x128 wave tiles and
+v_mfma_f32_16x16x32_f16, on the same LDS ring as the general loop; ragged
+edges are masked at the A and B loads (a partial last k-tile loads zeros past
+K) and at the C store.
 Checks:
 
 * against the fp64 oracle, |got - ref| <= 1e-2 * (|ref| + 1), on shapes that
   cover 1, 2, odd and even k-tile counts, tile / grouped / persistent orders
-  (more tiles than programs), padded leading dimensions, ragged M and N
-  (including a problem smaller than one wave tile, and padding columns that
-  must stay unwritten) and the fused steps;
+  (more tiles than programs), padded leading dimensions, ragged M, N and K
+  (including a problem smaller than one wave tile, a K below one k-tile, and
+  padding columns that must stay unwritten) and the fused steps;
 * bit-identity with the general loop at 8 waves (`w4x2`) and at 4 waves
   (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
   products in the same k order (in 32x32x16 or 16x16x32 steps), and the
@@ -20,8 +21,6 @@ Checks:
   instance and the general loop's fused instance, and the fused instance in
   persistent order.
 
-K not a multiple of 64 takes the general loop (test_gemm_gpu.py:
-test_ragged_edges, test_every_instance).
 """
 import numpy as np
 import pytest
@@ -74,6 +73,11 @@ CASES = [
     (1000, 1496, 768, tb.MAP_GROUPED_TILE, None, 8, 0),  # ragged, padding untouched
     (1300, 904, 512, tb.MAP_PERSISTENT_GROUPED, 7, 0, 0),  # 24 ragged tiles on 7
     (2000, 2056, 256, tb.MAP_GROUPED_TILE, None, 0, 8),  # 72 ragged tiles, XCD order
+    (512, 256, 200, tb.MAP_GROUPED_TILE, None, 0, 0),    # partial last k-tile (K % 64 = 8)
+    (256, 512, 40, tb.MAP_TILE, None, 8, 0),             # K below one k-tile, padded
+    (300, 520, 712, tb.MAP_GROUPED_TILE, None, 0, 0),    # ragged M, N and K (K % 64 = 8)
+    (1300, 904, 520, tb.MAP_PERSISTENT_GROUPED, 7, 0, 0),  # ragged all three, persistent
+    (768, 768, 1016, tb.MAP_GROUPED_TILE, None, 0, 0),   # K % 64 = 56
 ]
 
 
