@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the tb.matmul gfx950 path (one MI355X).
 
-Headline (BASELINE.json `metric`): TFLOP/s and fraction of dense FP16 MFMA
-peak on the 4096^3 f16 GEMM (`configs[2]`, the roofline config); a "step" is
+Headline metric: TFLOP/s and fraction of dense FP16 MFMA peak on the 4096^3
+f16 GEMM (the roofline workload of configs.py); a "step" is
 one GEMM launch over inputs already resident in HBM. The same JSON line also
 carries microseconds per launch for the small shapes and the split-K and
 persistent workloads (`extra`), the live roofline of the dominant kernel and

@@ -2,7 +2,8 @@
 
 The counterpart of the reference's tools/bench_stage1_fair.py: the same
 case list (its CASES, :120-324, plus its large-shape cases and this build's
-BASELINE workloads), the same CLI knobs and the same measurement protocol:
+benchmark workloads, configs.ALL), the same CLI knobs and the same
+measurement protocol:
 - every case is verified once before timing;
 - samples are taken in interleaved rounds, the two sides alternating who goes
   first (:750-809);
@@ -147,7 +148,7 @@ REFERENCE_CASES = (
 
 
 def _baseline_cases():
-    """The BASELINE workloads (f16 C = A*B), as FairCases."""
+    """The benchmark workloads of configs.py (f16 C = A*B), as FairCases."""
     from . import configs
     out = []
     for w in configs.ALL:

@@ -1,7 +1,7 @@
 """The interleaved fair benchmark (mini_triton_nvgpu_v1_amd/fair_bench.py),
 counterpart of the reference's tools/bench_stage1_fair.py.
 
-CPU: every case of the reference's case list (and of the BASELINE workloads)
+CPU: every case of the reference's case list (and of the benchmark workloads)
 goes through the plan pipeline and binds a compiled instance; the case
 descriptors agree with the reference's launch formulas; the statistics and
 case-selection rules behave like the reference's. GPU: a short run writes

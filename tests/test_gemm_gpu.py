@@ -3,7 +3,7 @@
 Inputs come from the oracle's seeded generator on the CPU and are uploaded;
 the kernel runs through the C ABI (libtb_gfx950.so); the result is checked
 per element with |got - ref| <= 1e-2 * (|ref| + 1) (f16 A/B, f32
-accumulation, the tolerance BASELINE.json states). Outputs are pre-filled
+accumulation: the path's stated tolerance). Outputs are pre-filled
 with NaN so an element the kernel fails to write fails the check.
 """
 import dataclasses

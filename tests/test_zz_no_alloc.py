@@ -62,7 +62,7 @@ def test_noalloc_matches_the_workspace_entry_point(device):
     import torch
     stream = torch.cuda.current_stream(device)
     cases = [
-        # the BASELINE split-K workload (8 MiB of partials), then a smaller
+        # the benchmark's split-K workload (8 MiB of partials), then a smaller
         # ragged one that reuses the front of the same scratch, then a fused
         # bias + GELU split-K, then a descriptor with no workspace at all
         _case("splitk_512x512x16384", 512, 512, 16384, 8, 0x5EED0005),
