@@ -16,6 +16,9 @@ Checks:
   (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
   products in the same k order (in 32x32x16 or 16x16x32 steps), and the
   test pins that the two MFMA shapes round it alike;
+* 40 seeded random ragged shapes (any M, N and K multiples of 8, every
+  program order, padded leading dimensions) against the oracle and bit for
+  bit against the 4-wave general loop;
 * every compile-time variant of the fused steps (activation x whether a
   clamp is set), against the oracle and bit-identical between the 16x16x32
   instance and the general loop's fused instance, and the fused instance in
@@ -183,3 +186,48 @@ def test_fused_steps_persistent(device):
     print(f"  violations={bad} max|err|={err:.3e}", flush=True)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
     assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+
+
+def _random_cases(n, seed):
+    """Seeded random shapes for the 16x16x32 instance: M any size, N and K
+    multiples of 8 (the C ABI's transport rule), every program order, padded
+    leading dimensions and the XCD order on some."""
+    import random
+    rng = random.Random(seed)
+    maps = [tb.MAP_TILE, tb.MAP_GROUPED_TILE, tb.MAP_PERSISTENT_TILE,
+            tb.MAP_PERSISTENT_GROUPED]
+    out = []
+    for i in range(n):
+        M, N, K = rng.randint(1, 1300), 8 * rng.randint(1, 160), 8 * rng.randint(1, 160)
+        mapping = rng.choice(maps)
+        tiles = -(-M // 256) * -(-N // 256)
+        programs = rng.randint(1, tiles) if mapping in maps[2:] else None
+        pad = rng.choice([0, 0, 8, 24])
+        xcd = 8 if mapping == tb.MAP_GROUPED_TILE and tiles % 8 == 0 and rng.random() < 0.5 else 0
+        out.append((M, N, K, mapping, programs, pad, xcd))
+    return out
+
+
+RANDOM_CASES = _random_cases(40, 0x5EED0780)
+
+
+@pytest.mark.parametrize("M,N,K,mapping,programs,pad,xcd", RANDOM_CASES,
+                         ids=[f"r{i}_{c[0]}x{c[1]}x{c[2]}" for i, c in enumerate(RANDOM_CASES)])
+def test_mfma16_random_shapes(M, N, K, mapping, programs, pad, xcd, device):
+    """Random ragged shapes on the 16x16x32 instance (whole-K and partial-K
+    builds): against the oracle, with padding columns untouched, and bit for
+    bit against the 4-wave general loop on the same shape."""
+    print(f"wide random {M}x{N}x{K} mapping {mapping} programs {programs} pad {pad} "
+          f"xcd {xcd}", flush=True)
+    A, B = oracle.config_inputs(M, N, K, 0x5EED0781 + M + 3 * N + 7 * K, oracle.NORMAL)
+    name16, got16 = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd, mfma16=True),
+                         A, B, device, pad)
+    assert name16 == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
+    if pad:
+        assert np.isnan(got16[:, N:].astype(np.float32)).all()
+    got16 = got16[:, :N]
+    bad, err, worst = oracle.check_tolerance(got16, oracle.gemm_f64(A, B), rtol=RTOL)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
+    name, got = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd), A, B, device, pad)
+    assert "16x16x32" not in name
+    assert np.array_equal(got16.view(np.uint16), got[:, :N].view(np.uint16)), name
