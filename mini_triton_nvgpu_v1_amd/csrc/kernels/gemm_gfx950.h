@@ -206,6 +206,9 @@ struct KernelEntry {
   // where its whole-K build carries no masking: the launcher picks it then
   // (null: fn handles every K)
   const void *fn_partial_k;
+  // threads per workgroup when the build adds waves of its own (producer
+  // waves); 0: num_waves * 64
+  int threads;
 };
 
 // Registry of compiled instances (defined in the instance files).

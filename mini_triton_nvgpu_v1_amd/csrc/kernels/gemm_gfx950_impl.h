@@ -1242,6 +1242,238 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   }
 }
 
+// ---- producer waves: f32-partial instances with dedicated load waves -------
+// The general loop's small-wave-tile instances spend their k-tiles waiting:
+// one wave per SIMD issues both the direct loads and the MFMAs, and a load
+// the texture path cannot yet accept stalls that wave's next MFMA. Here the
+// workgroup has twice the waves: waves NW .. 2NW-1 only issue the direct
+// loads (the general loop's load mapping, wave w - NW in the role of wave w)
+// and wait for them; waves 0 .. NW-1 only read fragments and run MFMAs. The
+// two halves meet at one barrier per k-tile:
+//  * before barrier it, a loader waits until its loads of k-tile it+1 have
+//    landed (vmcnt((STAGES-2) * LPT)), so after it k-tile it+1 is visible;
+//  * before barrier it, a compute wave has read all its fragments of k-tile
+//    it (the fence waits for them), so after it the loaders refill k-tile
+//    it's stage with k-tile it+STAGES.
+// A compute wave reads a whole k-tile's fragments right after each barrier
+// (double-buffered across k-tiles), so their latency runs under the previous
+// k-tile's MFMAs. Same LDS ring, swizzles, fragment reads, MFMA order and
+// staged f32 epilogue as the general instance of the same key: the partials
+// are bit-identical. Every wave takes every barrier (prologue, one per
+// k-tile, the epilogue's, the persistent loop's), so the counts match.
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES>
+__global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmParams p) {
+  using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES>;
+  constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
+                KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LPT = T::LPT;
+  static_assert(T::STAGED_F32_EPILOGUE, "f32 partials staged through LDS");
+  static_assert(KSTEPS == 4, "whole-k-tile fragment buffers sized for BK = 64");
+  __shared__ u32x4 lds[STAGES * T::STAGE];
+  auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = wave >= NW;
+  const u32x4 ra4 = rsrc_dwords(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
+  const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
+  const bool persistent =
+      p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
+  int prog = blockIdx.x;
+  const int nprog = gridDim.x;
+  if (p.xcds > 1 && (nprog % p.xcds) == 0)
+    prog = (prog % p.xcds) * (nprog / p.xcds) + prog / p.xcds;
+
+  for (int work = prog; work < p.total_work;
+       work += (persistent ? nprog : p.total_work)) {
+    int tile_m, tile_n, part;
+    map_program(p, work, tile_m, tile_n, part);
+    int kt0 = 0, nk = p.tiles_k;
+    if (p.mapping == kMapSplitK) {
+      // LowerPipelineToNVGPU.cpp:331-356 (contiguous k-tile range per split)
+      const int base = p.tiles_k / p.split_k, extra = p.tiles_k % p.split_k;
+      kt0 = part * base + (part < extra ? part : extra);
+      nk = base + (part < extra ? 1 : 0);
+    }
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int kt_end = kt0 + nk;
+    if (work != prog)
+      __syncthreads(); // the previous tile's staged epilogue has been read back
+
+    if (loader) { // ------------------------------------------------ loads
+      const int lw = wave - NW;
+      const int a_row0 = (lw * 64 + lane) / KCH;
+      const int a_pc = lane % KCH;
+      auto a_lchunk = [&](int i) {
+        return a_pc ^ (((a_row0 + i * T::A_ROWS_PER_LOAD) / T::A_PP) % KCH);
+      };
+      const int b_row0 = (lw * 64 + lane) / BNC;
+      const int b_pc = lane % BNC;
+      const int b_lc = b_pc ^ (4 * ((b_row0 / T::B_PP) % T::B_MAXPH));
+      const uint32_t a_vrow = (uint32_t)(m0 + a_row0) * (uint32_t)p.lda * 2u;
+      const int a_rows_left = p.M - m0 - a_row0;
+      const uint32_t b_voff = (n0 + b_lc * 8) < p.N
+                                  ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
+                                     (uint32_t)(n0 + b_lc * 8)) * 2u
+                                  : kOob;
+      auto issue_load = [&](int kt, int stage, int l) {
+        const int k0 = kt * BK;
+        const bool kt_ok = kt < kt_end;
+        const uint32_t a_lds =
+            (uint32_t)(uintptr_t)(TBK_LDS void *)stage_base(stage) + lw * 1024u;
+        if (l < LA) {
+          const int i = l;
+          const int lc = a_lchunk(i);
+          const bool ok =
+              kt_ok && (k0 + lc * 8) < p.K && i * T::A_ROWS_PER_LOAD < a_rows_left;
+          load_lds16(ra4, a_lds + i * NW * 1024u, ok ? a_vrow + lc * 16u : kOob,
+                     k0 * 2 + i * T::A_ROWS_PER_LOAD * p.lda * 2);
+        } else {
+          const int i = l - LA;
+          const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
+          const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
+          load_lds16(rb4, b_lds + i * NW * 1024u, (kt_ok && krow < p.K) ? b_voff : kOob,
+                     (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
+        }
+      };
+      auto issue_tile = [&](int kt, int stage) {
+#pragma unroll
+        for (int l = 0; l < LPT; ++l)
+          issue_load(kt, stage, l);
+      };
+#pragma unroll
+      for (int st = 0; st < STAGES; ++st)
+        issue_tile(kt0 + st, st);
+      wait_vmcnt<(STAGES - 1) * LPT>();
+      __syncthreads(); // k-tile 0 visible
+      int s = 0;
+      for (int it = 0; it < nk; ++it) {
+        wait_vmcnt<(STAGES - 2) * LPT>(); // k-tile it+1 landed
+        __syncthreads();                  // the compute waves' barrier of k-tile it
+        issue_tile(kt0 + it + STAGES, s); // stage s (k-tile it) is free
+        s = s + 1 == STAGES ? 0 : s + 1;
+      }
+      wait_vmcnt<0>(); // the zero loads past the end have landed too
+      __syncthreads(); // the epilogue's barrier
+      continue;
+    }
+
+    // -------------------------------------------------------------- compute
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int fr_a = wm * T::WTM + (lane & 31);
+    const int khalf = lane >> 5;
+    const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int tr_n = wn * T::WTN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = (f32x16){};
+    // a whole k-tile of fragments per buffer: [buffer][k step][tile]
+    half8 fa[2][KSTEPS][TM], fb[2][KSTEPS][TN];
+    auto read_tile = [&](int buf, int stage) {
+      const TBK_LDS u32x4 *As = (const TBK_LDS u32x4 *)stage_base(stage);
+      const TBK_LDS char *Bs = (const TBK_LDS char *)(As + T::A_STAGE);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int c = ks * 2 + khalf;
+          const int row = fr_a + i * 32;
+          fa[buf][ks][i] =
+              __builtin_bit_cast(half8, As[row * KCH + (c ^ ((row / T::A_PP) % KCH))]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = tr_n + j * 32;
+          half4 h[2];
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int k = ks * 16 + tr_k + 4 * r;
+            const int pc = (n >> 3) ^ (4 * ((k / T::B_PP) % T::B_MAXPH));
+            h[r] = __builtin_bit_cast(
+                half4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((TBK_LDS short4 *)(
+                           Bs + k * (BN * 2) + pc * 16 + (n & 7) * 2)));
+          }
+          fb[buf][ks][j] = (half8){h[0][0], h[0][1], h[0][2], h[0][3],
+                                   h[1][0], h[1][1], h[1][2], h[1][3]};
+        }
+      }
+    };
+    // C^T tile += B^T-fragment x A-fragment over the k-tile, k steps in order
+    auto mfma_tile = [&](int buf) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+        for (int q = 0; q < NMFMA; ++q) {
+          const int i = q / TN, j = q % TN;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[buf][ks][j], fa[buf][ks][i],
+                                                             acc[i][j], 0, 0, 0);
+        }
+    };
+    __syncthreads(); // k-tile 0 visible
+    read_tile(0, 0);
+    int s = 0;
+    for (int it = 0; it < nk; it += 2) { // two k-tiles: fixed fragment buffers
+      const int s1 = s + 1 == STAGES ? 0 : s + 1;
+      const int s2 = s1 + 1 == STAGES ? 0 : s1 + 1;
+      __syncthreads(); // k-tile it+1 visible; this wave's reads of k-tile it done
+      read_tile(1, s1);
+      mfma_tile(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (it + 1 < nk) {
+        __syncthreads();
+        read_tile(0, s2);
+        mfma_tile(1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      s = s2;
+    }
+
+    // f32 partials through LDS, as the general loop's staged f32 epilogue
+    float *base = p.ws + (size_t)part * (size_t)p.M * (size_t)p.ws_ld;
+    const int ld = p.ws_ld;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+    __syncthreads(); // the loaders drained; every compute wave finished its reads
+    TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * (32 * T::F32_ROWB);
+    constexpr int NLD = 32 / T::F32_RPI;
+    const int q = lane % T::F32_CPR;
+    const int col = n0 + wn * T::WTN + 4 * q;
+    const int rw = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row0 = m0 + wm * T::WTM + i * 32;
+      uint32_t off[NLD];
+#pragma unroll
+      for (int t = 0; t < NLD; ++t) {
+        const int row = row0 + t * T::F32_RPI + lane / T::F32_CPR;
+        off[t] = (row < p.M && col < p.N)
+                     ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                     : kOob;
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int cs = (8 * j + 2 * g + khalf) ^ ((rw / T::F32_RPP) % T::F32_XOR);
+          *(TBK_LDS f32x4 *)(wl + rw * T::F32_ROWB + cs * 16) =
+              (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                      acc[i][j][4 * g + 3]};
+        }
+#pragma unroll
+      for (int t = 0; t < NLD; ++t) {
+        const int r = t * T::F32_RPI + lane / T::F32_CPR;
+        const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
+        const f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
+        // written once, read once by the reduce: non-temporal (see the
+        // general loop)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t], 0,
+                                               kStoreNT);
+      }
+    }
+  }
+}
+
 // The 16x16x32 instance of the 4-wave 256x256x64 2-stage f16 configuration
 // (any M, N and K; tile, grouped or persistent order).
 template <bool EPI, bool KPART>

@@ -300,8 +300,21 @@ void deriveWaits(Module &m, const PassOptions &) {
         parseLatencyPlanAttr(need(op, "tb.latency_plan", "tb-assign-latencies"));
     PipelinePlan pp =
         parsePipelinePlanAttr(need(op, "tb.pipeline_plan", "tb-schedule-loops"));
+    // the instance flavour the lowering will bind (instanceKeyOf)
+    const ProgramMappingPlan pm = parseProgramMappingPlanAttr(
+        need(op, "tb.program_mapping_plan", "tb-build-program-mapping-plan"));
+    const ReductionPlan rd =
+        parseReductionPlanAttr(need(op, "tb.reduction_plan", "tb-build-program-mapping-plan"));
+    const EpiloguePlan ep =
+        parseEpiloguePlanAttr(need(op, "tb.epilogue_plan", "tb-build-c-register-plan"));
+    const bool splitK = pm.mappingKind == ProgramMappingKind::SplitK;
+    const int out = instanceOutOf(splitK, rd.kind == ReductionPlanKind::SplitKAtomic,
+                                  c.cScalar == ScalarKind::F16,
+                                  ep.initMode != AccumulatorInitMode::Zero);
+    const bool epi = !splitK && !epilogueRequestOf(ep).empty();
     op.attrs.erase("tb.wait_plan");
-    op.attrs["tb.async_plan"] = buildAsyncPlanAttr(deriveAsyncPlan(c, bm, tr, lat, pp));
+    op.attrs["tb.async_plan"] =
+        buildAsyncPlanAttr(deriveAsyncPlan(c, bm, tr, lat, pp, out, epi));
   });
 }
 

@@ -206,6 +206,8 @@ static void checkKernelWaits(const KernelContract &k, const InstanceKey &key) {
     differ("loads per thread", a.loadsPerThread, s.loadsPerThread);
   if (a.prologueTailLoads != s.prologueTailLoads)
     differ("prologue tail loads", a.prologueTailLoads, s.prologueTailLoads);
+  if (a.loaderWaves != s.loaderWaves)
+    differ("loader waves", a.loaderWaves, s.loaderWaves);
   if (a.waits.empty())
     throw Error("AsyncPlan has no waits");
   for (const WaitInfo &w : a.waits) {

@@ -67,15 +67,26 @@ InstanceKey instanceKeyOf(const tb_gemm_config &c) {
   k.wgm = c.wave_grid_m;
   k.wgn = c.wave_grid_n;
   k.stages = c.stages;
-  if (c.mapping == TB_MAP_SPLIT_K)
-    k.out = c.reduction == TB_RED_ATOMIC ? kInstOutF32Atomic : kInstOutF32Partial;
-  else if (c.c_dtype == TB_DTYPE_F16)
-    k.out = kInstOutF16;
-  else
-    k.out = c.acc_init == TB_ACC_INIT_LOAD_C ? kInstOutF32Accum : kInstOutF32Partial;
+  k.out = instanceOutOf(c.mapping == TB_MAP_SPLIT_K, c.reduction == TB_RED_ATOMIC,
+                        c.c_dtype == TB_DTYPE_F16, c.acc_init == TB_ACC_INIT_LOAD_C);
   k.epi = (c.epi_bias || c.epi_activation || c.epi_clamp) && c.mapping != TB_MAP_SPLIT_K;
   k.mfma = c.mfma;
   return k;
+}
+
+int instanceOutOf(bool splitK, bool atomicReduction, bool f16C, bool loadC) {
+  if (splitK)
+    return atomicReduction ? kInstOutF32Atomic : kInstOutF32Partial;
+  if (f16C)
+    return kInstOutF16;
+  return loadC ? kInstOutF32Accum : kInstOutF32Partial;
+}
+
+static bool producerTile(const InstanceKey &k) {
+#define TB_PRODUCER(BM, BN, BK, WGM, WGN, ST)                                          \
+  (k.bm == BM && k.bn == BN && k.bk == BK && k.wgm == WGM && k.wgn == WGN && k.stages == ST) ||
+  return TBK_PRODUCER_TILES(TB_PRODUCER) false;
+#undef TB_PRODUCER
 }
 
 InstanceSchedule instanceSchedule(const InstanceKey &k) {
@@ -94,6 +105,17 @@ InstanceSchedule instanceSchedule(const InstanceKey &k) {
   const int64_t nmfma = (k.bm / k.wgm / 32) * (k.bn / k.wgn / 32); // per 16-deep k step
   const int64_t lpt = (k.bm * (k.bk / 8) + k.bk * (k.bn / 8)) / threads;
   s.loadsPerThread = lpt;
+  if (k.out == kInstOutF32Partial && !k.epi && k.mfma == TB_MFMA_32X32X16 && producerTile(k)) {
+    // the loaders issue with the compute waves' thread count: wave w - NW
+    // issues wave w's loads
+    s.issue = "producer_waves";
+    s.loaderWaves = k.wgm * k.wgn;
+    s.prologueTailLoads = lpt;
+    s.vmPrologue = (k.stages - 1) * lpt;
+    s.vmLoop = (k.stages - 2) * lpt;
+    s.lgkmLoop = -1;
+    return s;
+  }
   if (nmfma >= 4) {
     s.issue = "slot_spread";
     const int64_t nslot = (k.bk / 16) * nmfma, after = nmfma / 2;

@@ -42,6 +42,9 @@ std::string instanceName(const InstanceKey &k);
 // from C's type, C's initialisation and the reduction; split-K partials take
 // the fused steps in the reduction, so they bind the plain instance.
 InstanceKey instanceKeyOf(const tb_gemm_config &c);
+// The output mode instanceKeyOf binds, from the facts that decide it (the
+// plans state them before the lowering flattens them into tb_gemm_config).
+int instanceOutOf(bool splitK, bool atomicReduction, bool f16C, bool loadC);
 // How an instance issues its direct-to-LDS loads, and the s_waitcnt depths
 // that follow (the kernel's GemmTile slot geometry, restated on the host):
 //  * "slot_spread": wave tiles of 4+ MFMAs per k step; the k-tile is cut
@@ -52,13 +55,19 @@ InstanceKey instanceKeyOf(const tb_gemm_config &c);
 //  * "burst": smaller wave tiles; a refill is issued whole right after the
 //    barrier, and the prologue issues all S k-tiles;
 //  * "exact_tile_slots": the 16x16x32 instance (k-tiles 0 and 1 whole in the
-//    prologue; every barrier waits for all loads and LDS reads).
+//    prologue; every barrier waits for all loads and LDS reads);
+//  * "producer_waves": the f32-partial tiles of TBK_PRODUCER_TILES, whose
+//    workgroup adds `loaderWaves` waves that only issue the loads: they issue
+//    all S k-tiles in the prologue and, at each barrier, wait for the next
+//    k-tile only (vmcnt (S-1) and (S-2) loads-per-thread), then refill the
+//    stage the barrier freed whole.
 // vmcnt at the prologue wait = (S-2) loads-per-thread + prologueTailLoads,
 // vmcnt at the per-k-tile barrier = (S-2) loads-per-thread; lgkmcnt -1 = none.
 struct InstanceSchedule {
   std::string issue;
   int64_t loadsPerThread = 0, prologueTailLoads = 0, refillSpreadSlots = 0;
   int64_t vmPrologue = 0, vmLoop = 0, lgkmLoop = -1;
+  int64_t loaderWaves = 0; // load-only waves beside the wave grid's
 };
 InstanceSchedule instanceSchedule(const InstanceKey &k);
 

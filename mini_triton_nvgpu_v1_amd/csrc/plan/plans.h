@@ -625,10 +625,13 @@ struct AsyncPlan {
   // waits' depths follow (instances.h, InstanceSchedule)
   std::string issueSchedule;
   int64_t loadsPerThread = 0, prologueTailLoads = 0, refillSpreadSlots = 0;
+  int64_t loaderWaves = 0; // load-only waves beside the wave grid ("producer_waves")
 };
+// `out` (InstanceOut) and `epi` name the instance flavour the lowering binds
+// (instanceOutOf), which with the tile decides the issue schedule.
 AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
                           const TransportPlan &tr, const LatencyPlan &lat,
-                          const PipelinePlan &pp);
+                          const PipelinePlan &pp, int out, bool epi);
 AttrP buildAsyncPlanAttr(const AsyncPlan &p);
 AsyncPlan parseAsyncPlanAttr(const Attr &a);
 

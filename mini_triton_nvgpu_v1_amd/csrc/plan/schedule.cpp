@@ -580,6 +580,7 @@ template <class V> void fields(V &v, AsyncPlan &p) {
   v("loads_per_thread", p.loadsPerThread);
   v("prologue_tail_loads", p.prologueTailLoads);
   v("refill_spread_slots", p.refillSpreadSlots);
+  v("loader_waves", p.loaderWaves);
 }
 
 // Loads one thread issues per k group: each 16-byte vector of the A and B
@@ -607,7 +608,7 @@ static int64_t loadsPerThread(const KernelConfig &c, const TransportPlan &tr) {
 // barrier frees have returned).
 AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
                           const TransportPlan &tr, const LatencyPlan &,
-                          const PipelinePlan &pp) {
+                          const PipelinePlan &pp, int out, bool epi) {
   AsyncPlan p;
   const int64_t S = c.requestedStages, lpt = loadsPerThread(c, tr);
   InstanceKey key;
@@ -618,6 +619,8 @@ AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
   key.wgm = grid.first;
   key.wgn = grid.second;
   key.stages = S;
+  key.out = out;
+  key.epi = epi ? 1 : 0;
   key.mfma = c.mmaKind == MmaKind::Mfma16x16x32F16 ? TB_MFMA_16X16X32 : TB_MFMA_32X32X16;
   const InstanceSchedule sched = instanceSchedule(key);
   if (sched.loadsPerThread != lpt)
@@ -630,6 +633,7 @@ AsyncPlan deriveAsyncPlan(const KernelConfig &c, const BufferModel &m,
   p.loadsPerThread = lpt;
   p.prologueTailLoads = sched.prologueTailLoads;
   p.refillSpreadSlots = sched.refillSpreadSlots;
+  p.loaderWaves = sched.loaderWaves;
   std::map<int64_t, const PipelinePlacement *> place;
   for (const PipelinePlacement &pl : pp.placements)
     place[pl.opId] = &pl;

@@ -286,7 +286,8 @@ static int launch_impl(const tb_gemm_desc *d, const void *a, const void *b, void
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   void *args[] = {&p};
-  const dim3 grid((unsigned)cf.num_programs), block((unsigned)(cf.num_waves * 64));
+  const dim3 grid((unsigned)cf.num_programs),
+      block((unsigned)(d->entry->threads ? d->entry->threads : cf.num_waves * 64));
   const void *fn = d->entry->fn_partial_k && cf.k % cf.block_k ? d->entry->fn_partial_k
                                                                : d->entry->fn;
   if (int rc = check_hip(hipLaunchKernel(fn, grid, block, args, 0, s),

@@ -61,9 +61,10 @@ int main(int argc, char **argv) {
         // name, then the s_waitcnt depths the plan states for it
         for (const tb::InstanceKey &k : tb::gfx950Instances()) {
           const tb::InstanceSchedule s = tb::instanceSchedule(k);
-          std::printf("%s %s vmcnt_prologue=%lld vmcnt_loop=%lld lgkmcnt_loop=%lld\n",
+          std::printf("%s %s vmcnt_prologue=%lld vmcnt_loop=%lld lgkmcnt_loop=%lld "
+                      "loader_waves=%lld\n",
                       tb::instanceName(k).c_str(), s.issue.c_str(), (long long)s.vmPrologue,
-                      (long long)s.vmLoop, (long long)s.lgkmLoop);
+                      (long long)s.vmLoop, (long long)s.lgkmLoop, (long long)s.loaderWaves);
         }
         return 0;
       }

@@ -377,9 +377,10 @@ def test_ir_type_and_op_verifiers():
     assert p.returncode == 1 and "requires module attr `tb.num-ctas`" in p.stderr
 
 
-def _listed_instances():
+def _listed_instances(loader_waves=False):
     """tb-opt --list-instances: name -> (issue schedule, vmcnt prologue,
-    vmcnt loop, lgkmcnt loop) from the host-side table."""
+    vmcnt loop, lgkmcnt loop) from the host-side table; with loader_waves,
+    name -> the load-only waves the instance adds to its wave grid."""
     p = subprocess.run([str(TB_OPT), "--list-instances"], capture_output=True,
                        text=True, timeout=60, check=True)
     out = {}
@@ -387,8 +388,9 @@ def _listed_instances():
         name, issue, *kv = line.split()
         vals = dict(x.split("=") for x in kv)
         assert name not in out
-        out[name] = (issue, int(vals["vmcnt_prologue"]), int(vals["vmcnt_loop"]),
-                     int(vals["lgkmcnt_loop"]))
+        out[name] = int(vals["loader_waves"]) if loader_waves else (
+            issue, int(vals["vmcnt_prologue"]), int(vals["vmcnt_loop"]),
+            int(vals["lgkmcnt_loop"]))
     return out
 
 
@@ -415,11 +417,21 @@ def test_tb_opt_instance_table_equals_the_kernel_registry():
     assert sorted(listed) == sorted(compiled)
     for name, (issue, vmp, vml, lgkm) in listed.items():
         assert (vmp, vml, lgkm) == compiled[name], (name, issue)
-    # the three issue schedules all occur, and differ in the prologue wait
-    assert {v[0] for v in listed.values()} == {"slot_spread", "burst", "exact_tile_slots"}
+    # the four issue schedules all occur, and differ in the prologue wait
+    assert {v[0] for v in listed.values()} == {"slot_spread", "burst", "exact_tile_slots",
+                                               "producer_waves"}
     assert listed["tb_gemm_gfx950_256x256x64_w4x2_s2_out0"][1:] == (4, 0, -1)
     assert listed["tb_gemm_gfx950_128x64x64_w4x1_s3_out1"][:2] == ("burst", 12)
     assert listed["tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"][1:] == (16, 0, 0)
+    # the split-K tile's partial instance: 8 load-only waves that issue all 3
+    # k-tiles (3 loads per lane each) up front and wait for one at a time; its
+    # other output modes keep the general loop (burst: 32x32 wave tiles)
+    pw = "tb_gemm_gfx950_128x64x64_w4x2_s3_out1"
+    assert listed[pw] == ("producer_waves", 6, 3, -1)
+    waves = _listed_instances(loader_waves=True)
+    assert waves[pw] == 8
+    assert {n for n, v in waves.items() if v} == {pw}
+    assert listed["tb_gemm_gfx950_128x64x64_w4x2_s3_out0"] == ("burst", 6, 3, -1)
     L = tb.lib()
     import ctypes
     x = ctypes.c_int32()
