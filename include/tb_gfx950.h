@@ -96,7 +96,9 @@ typedef struct tb_gemm_config {
   int32_t c_dtype;       /* TB_DTYPE_F16 | TB_DTYPE_F32 (A, B are f16) */
   int32_t acc_init;      /* TB_ACC_INIT_* */
   int64_t block_m, block_n, block_k; /* macro tile (tileM/N/K) */
-  int64_t num_waves;     /* wavefronts per workgroup (tb.num-warps) */
+  int64_t num_waves;     /* MFMA wavefronts per workgroup (tb.num-warps); an
+                          * instance built with producer waves launches as many
+                          * load-only waves again (the plan's loader_waves) */
   int64_t wave_grid_m, wave_grid_n; /* WarpDecompositionPlan warpGrid */
   int64_t stages;        /* LDS stages (requested stages) */
   int32_t mapping;       /* TB_MAP_* */
