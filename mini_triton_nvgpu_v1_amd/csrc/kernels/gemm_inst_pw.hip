@@ -11,7 +11,7 @@ namespace tbk {
    "tb_gemm_gfx950_" #BM "x" #BN "x" #BK "_w" #WGM "x" #WGN "_s" #ST "_out1",     \
    (ST - 1) * GemmTile<BM, BN, BK, WGM, WGN, ST>::LPT,                            \
    (ST - 2) * GemmTile<BM, BN, BK, WGM, WGN, ST>::LPT, -1, nullptr,               \
-   2 * WGM * WGN * 64}
+   2 * WGM * WGN * 64},
 static const KernelEntry kProducer[] = {TBK_PRODUCER_TILES(TBK_PW_ENTRY)};
 #undef TBK_PW_ENTRY
 const KernelEntry *entries_producer(int *n) {

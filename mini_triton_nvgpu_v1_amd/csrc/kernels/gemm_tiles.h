@@ -35,8 +35,10 @@
 // plain f32 C) is built with producer waves (gemm_kernel_pw: as many load-only
 // waves as compute waves), in place of the general loop's build of the same
 // key. Listed where that measured faster: 128x64x64 on 8 waves, 3 stages,
-// the split-K workload's tile (512^2 x 16384 in 8 splits: 19.1 -> 17.5 us
-// per call on one box).
+// the split-K workload's tile (512^2 x 16384 in 8 splits: 18.9 -> 16.8 us
+// per call). The same build on 4 stages, or on 2x2 and 4x1 wave grids, ran
+// 0.2-1.4 us slower per call there. Entries are not separated: each X supplies its own
+// separator.
 #define TBK_PRODUCER_TILES(X) X(128, 64, 64, 4, 2, 3)
 
 #define TBK_TILES_64x64(X) \
