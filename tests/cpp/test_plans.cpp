@@ -265,11 +265,34 @@ static void instances() {
   CHECK_EQ(s16.vmPrologue, 16);
   CHECK_EQ(s16.vmLoop, 0);
   CHECK_EQ(s16.lgkmLoop, 0);
-  // a 3-stage general instance: (S - 2) loads-per-thread tiles stay in flight
-  InstanceKey k3{128, 64, 64, 4, 2, 1, 3, 0, 0};
+  // the split-K tile's f32-partial instance is the producer-wave build: 8
+  // load-only waves, 3 loads per lane per k-tile, all 3 k-tiles issued in the
+  // prologue, (S - 2) k-tiles in flight at each barrier
+  InstanceKey k3{128, 64, 64, 4, 2, kInstOutF32Partial, 3, 0, TB_MFMA_32X32X16};
   CHECK(hasGfx950Instance(k3));
   const InstanceSchedule s3 = instanceSchedule(k3);
+  CHECK(s3.issue == "producer_waves");
+  CHECK_EQ(s3.loaderWaves, 8);
+  CHECK_EQ(s3.loadsPerThread, 3);
+  CHECK_EQ(s3.vmPrologue, (3 - 1) * s3.loadsPerThread);
   CHECK_EQ(s3.vmLoop, (3 - 2) * s3.loadsPerThread);
+  // the same tile's f16 and C += A*B instances keep the general loop (32x32
+  // wave tiles: burst refills), with the same waits and no loader waves
+  for (int out : {kInstOutF16, kInstOutF32Accum}) {
+    InstanceKey kg = k3;
+    kg.out = out;
+    const InstanceSchedule sg = instanceSchedule(kg);
+    CHECK(sg.issue == "burst");
+    CHECK_EQ(sg.loaderWaves, 0);
+    CHECK_EQ(sg.vmPrologue, s3.vmPrologue);
+    CHECK_EQ(sg.vmLoop, s3.vmLoop);
+  }
+  // the output mode the plan derives for each (mapping, reduction, C, init)
+  CHECK_EQ(instanceOutOf(true, false, true, false), kInstOutF32Partial);
+  CHECK_EQ(instanceOutOf(true, true, false, true), kInstOutF32Atomic);
+  CHECK_EQ(instanceOutOf(false, false, true, false), kInstOutF16);
+  CHECK_EQ(instanceOutOf(false, false, false, false), kInstOutF32Partial);
+  CHECK_EQ(instanceOutOf(false, false, false, true), kInstOutF32Accum);
   // every listed instance names its shape and is unique
   std::set<std::string> names;
   for (const InstanceKey &k : gfx950Instances())
