@@ -127,6 +127,13 @@ def _cfg(**kw):
     (dict(epi_activation=tb.ACT_RELU, c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_LOAD_C,
           mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_ATOMIC, num_programs=2),
      "whole sum"),
+    # 32-bit buffer offsets: every operand and the workspace under 2 GiB
+    (dict(m=32768, k=32768, lda=32768, num_programs=0), "larger than 2 GiB"),  # A = 2 GiB
+    (dict(k=32768, lda=32768, n=32768, ldb=32768, ldc=32768, num_programs=0),
+     "larger than 2 GiB"),  # B = 2 GiB
+    (dict(m=8192, n=8192, ldb=8192, ldc=8192, mapping=tb.MAP_SPLIT_K, split_k=8,
+          reduction=tb.RED_WORKSPACE, k=256, lda=256, num_programs=0),
+     "larger than 2 GiB"),  # 8 f32 planes of 8192^2 = 2 GiB
 ])
 def test_descriptor_validation_errors(kw, msg):
     with pytest.raises(tb.TbError, match=msg):
