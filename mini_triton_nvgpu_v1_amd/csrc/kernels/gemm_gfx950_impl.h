@@ -23,8 +23,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Buffer descriptor dword3 for gfx9-family raw buffers (stride 0, untyped,
 // bounds checked against num_records).
 static constexpr int kBufferFlags = 0x00020000;
-// Any offset at or above num_records reads zero / drops the store; the host
-// guarantees every operand spans fewer than 2^31 bytes.
+// Any offset at or above num_records reads zero / drops the store. A, C and
+// the split-K partials are addressed through windows that start at the
+// tile's first row (rows_at), so only a tile's rows must span fewer than
+// 2^31 bytes; B is addressed whole (the host checks both).
 static constexpr uint32_t kOob = 0x80000000u;
 // Cache-policy operand of a buffer store that sets nt (non-temporal) on gfx950.
 static constexpr int kStoreNT = 2;
@@ -81,11 +83,28 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-// Raw buffer descriptor as four dwords for inline asm operands.
+// Raw buffer descriptor as four dwords for inline asm operands ("s"): the
+// address and size are wave-uniform, and readfirstlane says so to the
+// compiler, which otherwise keeps a base computed from the tile index in
+// vector registers.
 __device__ __forceinline__ u32x4 rsrc_dwords(const void *p, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(p);
-  return (u32x4){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes,
-                 (uint32_t)kBufferFlags};
+  return (u32x4){(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), (uint32_t)kBufferFlags};
+}
+
+// Row row0 of a row-major matrix of `ld` elements of `esize` bytes per row:
+// the base of a tile's buffer window (a 64-bit address), so the 32-bit
+// offsets a tile forms inside it stay small however large the matrix is.
+__device__ __forceinline__ const void *rows_at(const void *p, int row0, int ld, int esize) {
+  return static_cast<const char *>(p) + (size_t)row0 * (size_t)ld * (size_t)esize;
+}
+// num_records of that window: the rows from row0 to the matrix end, capped
+// below kOob (the masks keep a tile inside its own rows).
+__device__ __forceinline__ uint32_t rows_bytes(int row0, int rows, int ld, int esize) {
+  const uint64_t b = (uint64_t)(rows - row0) * (uint64_t)ld * (uint64_t)esize;
+  return b < (uint64_t)kOob ? (uint32_t)b : kOob - 16u;
 }
 
 // s_waitcnt vmcnt(N) (expcnt / lgkmcnt untouched), gfx9 encoding.
@@ -354,7 +373,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
   const int a_rows_left = p.M - m0 - a_row0;
   const uint32_t a_voff =
-      a_rows_left > 0 ? ((uint32_t)(m0 + a_row0) * (uint32_t)p.lda + a_lc * 8) * 2u : kOob;
+      a_rows_left > 0 ? ((uint32_t)a_row0 * (uint32_t)p.lda + a_lc * 8) * 2u : kOob;
   const int b_row0 = (wave * 64 + lane) >> 5; // 0 .. 7: (k / 8) % 2 = round % 2
   const int b_lc = (lane & 31) ^ (4 * (b_row0 & 3));
   const uint32_t b_voff0 =
@@ -367,7 +386,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
           : kOob;
   const uint32_t a_round = 32u * (uint32_t)p.lda * 2u, b_round = 8u * (uint32_t)p.ldb * 2u;
   const uint32_t a_ktile = BK * 2u, b_ktile = BK * 2u * (uint32_t)p.ldb;
-  const uint32_t a_bytes = (uint32_t)p.M * (uint32_t)p.lda * 2u;
+  const void *a_tile = rows_at(p.A, m0, p.lda, 2); // A's window starts at row m0
+  const uint32_t a_bytes = rows_bytes(m0, p.M, p.lda, 2);
   const uint32_t b_bytes = (uint32_t)p.K * (uint32_t)p.ldb * 2u;
   const uint32_t wlds = lds0 + wave * 1024u;
   const int k_rounds = (p.K - kfull * BK) / 8; // B rounds of the partial k-tile
@@ -492,8 +512,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 
   // prologue: k-tiles 0 and 1 in flight, wait for 0, run it up to its barrier
   {
-    const u32x4 ra = rsrc_dwords(p.A, a_bytes), rb = rsrc_dwords(p.B, b_bytes);
-    const u32x4 ra1 = rsrc_dwords(p.A, nk > 1 ? a_bytes : 0u);
+    const u32x4 ra = rsrc_dwords(a_tile, a_bytes), rb = rsrc_dwords(p.B, b_bytes);
+    const u32x4 ra1 = rsrc_dwords(a_tile, nk > 1 ? a_bytes : 0u);
     const u32x4 rb1 = rsrc_dwords(p.B, nk > 1 ? b_bytes : 0u);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
@@ -516,7 +536,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   auto body = [&](int it, auto stage, auto kmask_c) {
     constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
-    const u32x4 ra = rsrc_dwords(p.A, ok ? a_bytes : 0u);
+    const u32x4 ra = rsrc_dwords(a_tile, ok ? a_bytes : 0u);
     const u32x4 rb = rsrc_dwords(p.B, ok ? b_bytes : 0u);
     // k-tile it+1 landed (this wave's part), and this wave's reads of stage
     // S are done (the last A rows of k step 1 are read in k step 0 but only
@@ -592,7 +612,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // clamp bounds: -inf / +inf for a clamp that is off
   const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
   const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
-  const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
+  // C's window starts at row m0
+  const __amdgpu_buffer_rsrc_t rc =
+      make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
   const int q = el & 15;
   // One 16-row block of the wave tile at a time: its 8 tiles go into LDS,
   // then its 16 rows come back and go out, so the stores of block i run
@@ -632,9 +654,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
         if ((rr >> 3) & 1)
           v = (u32x4){v[2], v[3], v[0], v[1]};
         const int row = m0 + wm * 128 + rr, col = n0 + wn * 128 + 8 * q;
-        const uint32_t off = row < p.M && col < p.N
-                                 ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u
-                                 : kOob;
+        const uint32_t off =
+            row < p.M && col < p.N
+                ? ((uint32_t)(wm * 128 + rr) * (uint32_t)p.ldc + (uint32_t)col) * 2u
+                : kOob;
         // non-temporal (nt): C is written once and not read again by this
         // kernel; measured 0.7% faster at 4096^3 than the default policy
         __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
@@ -667,7 +690,6 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
-  const u32x4 ra4 = rsrc_dwords(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
   const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
 
   const bool persistent =
@@ -733,7 +755,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     f32x4 c_pre[PREFETCH_C ? TM : 1][PREFETCH_C ? TN : 1][4];
     if constexpr (PREFETCH_C) {
       const __amdgpu_buffer_rsrc_t rc =
-          make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 4u);
+          make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
       const int row0 = m0 + wm * T::WTM + (lane & 31);
       const int col0 = n0 + wn * T::WTN + 4 * khalf;
 #pragma unroll
@@ -743,9 +765,10 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int row = row0 + i * 32, col = col0 + j * 32 + 8 * g;
-            const uint32_t off = (row < p.M && col < p.N)
-                                     ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 4u
-                                     : kOob;
+            const uint32_t off =
+                (row < p.M && col < p.N)
+                    ? ((uint32_t)(row - m0) * (uint32_t)p.ldc + (uint32_t)col) * 4u
+                    : kOob;
             c_pre[i][j][g] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
           }
@@ -753,8 +776,9 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 
     // The k-dependent part of each global address is wave-uniform and rides
     // in the scalar offset; a row, column or k range outside the problem gets
-    // the vector offset kOob, which loads zero.
-    const uint32_t a_vrow = (uint32_t)(m0 + a_row0) * (uint32_t)p.lda * 2u;
+    // the vector offset kOob, which loads zero. A's window starts at row m0.
+    const u32x4 ra4 = rsrc_dwords(rows_at(p.A, m0, p.lda, 2), rows_bytes(m0, p.M, p.lda, 2));
+    const uint32_t a_vrow = (uint32_t)a_row0 * (uint32_t)p.lda * 2u;
     const int a_rows_left = p.M - m0 - a_row0; // round i valid iff i*rows < left
     const uint32_t b_voff = (n0 + b_lc * 8) < p.N
                                 ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
@@ -1044,7 +1068,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         }
       }
       const __amdgpu_buffer_rsrc_t rc =
-          make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
+          make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
       const int q = lane % T::EPI_CPR;
 #pragma unroll
       for (int it2 = 0; it2 < T::WTM / T::EPI_RPI; ++it2) {
@@ -1055,14 +1079,15 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           v = (u32x4){v[2], v[3], v[0], v[1]};
         const int row = m0 + wm * T::WTM + r;
         const int col = n0 + wn * T::WTN + 8 * q;
-        const uint32_t off = (row < p.M && col < p.N)
-                                 ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u
-                                 : kOob;
+        const uint32_t off =
+            (row < p.M && col < p.N)
+                ? ((uint32_t)(row - m0) * (uint32_t)p.ldc + (uint32_t)col) * 2u
+                : kOob;
         __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, 0);
       }
     } else if constexpr (OUT == kOutF16) {
       const __amdgpu_buffer_rsrc_t rc =
-          make_rsrc(p.C, (uint32_t)p.M * (uint32_t)p.ldc * 2u);
+          make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = crow_base + i * 32;
@@ -1073,7 +1098,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
             const int col = ccol_base + j * 32 + 8 * g;
             const bool ok = row < p.M && col < p.N;
             const uint32_t off =
-                ok ? ((uint32_t)row * (uint32_t)p.ldc + (uint32_t)col) * 2u : kOob;
+                ok ? ((uint32_t)(row - m0) * (uint32_t)p.ldc + (uint32_t)col) * 2u : kOob;
             const _Float16 h0 = (_Float16)acc[i][j][4 * g + 0];
             const _Float16 h1 = (_Float16)acc[i][j][4 * g + 1];
             const _Float16 h2 = (_Float16)acc[i][j][4 * g + 2];
@@ -1101,7 +1126,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                         : reinterpret_cast<float *>(p.C);
       const int ld = OUT == kOutF32Partial ? p.ws_ld : p.ldc;
       const __amdgpu_buffer_rsrc_t rc =
-          make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+          make_rsrc(rows_at(base, m0, ld, 4), rows_bytes(m0, p.M, ld, 4));
       __syncthreads(); // every wave drained its loads and finished its reads
       TBK_LDS char *wl =
           (TBK_LDS char *)(TBK_LDS void *)lds + wave * (32 * T::F32_ROWB);
@@ -1117,7 +1142,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         for (int t = 0; t < NLD; ++t) {
           const int row = row0 + t * T::F32_RPI + lane / T::F32_CPR;
           off[t] = (row < p.M && col < p.N)
-                       ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                       ? ((uint32_t)(row - m0) * (uint32_t)ld + (uint32_t)col) * 4u
                        : kOob;
         }
         f32x4 old[OUT == kOutF32Accum ? NLD : 1];
@@ -1166,11 +1191,11 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                         : reinterpret_cast<float *>(p.C);
       const int ld = OUT == kOutF32Partial ? p.ws_ld : p.ldc;
       const __amdgpu_buffer_rsrc_t rc =
-          make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+          make_rsrc(rows_at(base, m0, ld, 4), rows_bytes(m0, p.M, ld, 4));
       auto c_off = [&](int i, int j, int g) -> uint32_t {
         const int row = crow_base + i * 32, col = ccol_base + j * 32 + 8 * g;
         return (row < p.M && col < p.N)
-                   ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                   ? ((uint32_t)(row - m0) * (uint32_t)ld + (uint32_t)col) * 4u
                    : kOob;
       };
       // C += A*B reads the prior C first. All loads of a group of tiles (the
@@ -1274,7 +1299,6 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = wave >= NW;
-  const u32x4 ra4 = rsrc_dwords(p.A, (uint32_t)p.M * (uint32_t)p.lda * 2u);
   const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
@@ -1309,7 +1333,10 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
       const int b_row0 = (lw * 64 + lane) / BNC;
       const int b_pc = lane % BNC;
       const int b_lc = b_pc ^ (4 * ((b_row0 / T::B_PP) % T::B_MAXPH));
-      const uint32_t a_vrow = (uint32_t)(m0 + a_row0) * (uint32_t)p.lda * 2u;
+      // A's window starts at row m0
+      const u32x4 ra4 =
+          rsrc_dwords(rows_at(p.A, m0, p.lda, 2), rows_bytes(m0, p.M, p.lda, 2));
+      const uint32_t a_vrow = (uint32_t)a_row0 * (uint32_t)p.lda * 2u;
       const int a_rows_left = p.M - m0 - a_row0;
       const uint32_t b_voff = (n0 + b_lc * 8) < p.N
                                   ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
@@ -1433,7 +1460,8 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
     // f32 partials through LDS, as the general loop's staged f32 epilogue
     float *base = p.ws + (size_t)part * (size_t)p.M * (size_t)p.ws_ld;
     const int ld = p.ws_ld;
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc(base, (uint32_t)p.M * (uint32_t)ld * 4u);
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(rows_at(base, m0, ld, 4), rows_bytes(m0, p.M, ld, 4));
     __syncthreads(); // the loaders drained; every compute wave finished its reads
     TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * (32 * T::F32_ROWB);
     constexpr int NLD = 32 / T::F32_RPI;
@@ -1448,7 +1476,7 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
       for (int t = 0; t < NLD; ++t) {
         const int row = row0 + t * T::F32_RPI + lane / T::F32_CPR;
         off[t] = (row < p.M && col < p.N)
-                     ? ((uint32_t)row * (uint32_t)ld + (uint32_t)col) * 4u
+                     ? ((uint32_t)(row - m0) * (uint32_t)ld + (uint32_t)col) * 4u
                      : kOob;
       }
 #pragma unroll
