@@ -528,3 +528,14 @@ def test_no_plan_legal_configuration_lacks_a_kernel(bm, bn):
                         f"tb_gemm_gfx950_{bm}x{bn}x{bk}_w{grid[0]}x{grid[1]}_s{stages}_")
     if (bm, bn) not in ((96, 64), (160, 96)):
         assert bound > 0
+
+
+def test_plan_over_operands_past_2gib():
+    """The plan pipeline and the C ABI bind operands of several GiB (A and B
+    past 2 GiB each): the kernels address them in per-tile windows."""
+    w = configs.Workload("big", 139264, 4096, 270336, 1, 0, (256, 256, 64), num_waves=4)
+    desc = tb.plan_from_mlir(w.mlir())
+    assert desc.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
+    cfg = desc.config
+    assert (cfg.m, cfg.n, cfg.k) == (139264, 4096, 270336)
+    assert cfg.m * cfg.lda * 2 > 1 << 31 and cfg.k * cfg.ldb * 2 > 1 << 31
