@@ -243,3 +243,42 @@ def test_tensor_operands_checked_against_the_descriptor():
     short = torch.zeros(sk.workspace_bytes // 4 - 1, dtype=torch.float32)
     with pytest.raises(tb.TbError, match="workspace: the descriptor touches"):
         sk.launch(As, Bs, Cs, short)
+
+
+def test_descriptors_and_errors_from_many_threads():
+    """Descriptor creation and the plan pipeline run concurrently from host
+    threads (ctypes releases the GIL for the library's calls), and each
+    thread reads its own error message: tb_last_error is thread-local. Every
+    thread alternates a valid descriptor, a plan, and a refusal whose message
+    is specific to that thread."""
+    import threading
+    bad = [(dict(wave_grid_m=1), "wave grid"), (dict(lda=16), "leading dimensions"),
+           (dict(num_programs=7), "launch formula"), (dict(epi_bias=3), "epi_bias"),
+           (dict(k=36, lda=36), "multiples of 8"), (dict(mapping=9), "unknown mapping"),
+           (dict(epi_clamp=4), "unknown bits"), (dict(m=0), "positive")]
+    good_name = tb.GemmDesc.from_config(_cfg()).kernel_name
+    mlir = configs.RAGGED.mlir()
+    plan_name = tb.plan_from_mlir(mlir).kernel_name
+    failures = []
+
+    def worker(i):
+        kw, msg = bad[i % len(bad)]
+        try:
+            for _ in range(40):
+                assert tb.GemmDesc.from_config(_cfg()).kernel_name == good_name
+                try:
+                    tb.GemmDesc.from_config(_cfg(**kw))
+                    failures.append(f"thread {i}: no error for {kw}")
+                except tb.TbError as e:
+                    if msg not in str(e):
+                        failures.append(f"thread {i}: expected '{msg}', got '{e}'")
+                assert tb.plan_from_mlir(mlir).kernel_name == plan_name
+        except Exception as e:  # noqa: BLE001 - reported below
+            failures.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not failures, "\n".join(failures[:10])
