@@ -121,10 +121,10 @@ const char *tb_last_error(void);
 
 /* Build a descriptor from a flattened config; selects the gfx950 kernel
  * instance. Replaces LowerPipelineToNVGPU.cpp:2624-2732 (contract
- * validation + gpu.func emission). Operands of any size are accepted as long
- * as one tile's rows of A and C (block_m rows) and one k-tile's rows of B
- * (block_k rows) each span less than 1 GiB: the kernels address every
- * operand through per-tile windows with 32-bit offsets inside. */
+ * validation + gpu.func emission). A, C and the split-K workspace may be of
+ * any size as long as one tile's rows of A and C (block_m rows) span less
+ * than 1 GiB: the kernels address them through per-tile windows with 32-bit
+ * offsets inside. B must span less than 2 GiB. */
 int tb_desc_create(const tb_gemm_config *cfg, tb_gemm_desc **out);
 
 /* Run the tb plan pipeline (tb-verify-scope ... tb-verify-pipeline-mainline-

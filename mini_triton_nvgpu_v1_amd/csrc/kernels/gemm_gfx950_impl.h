@@ -25,9 +25,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 static constexpr int kBufferFlags = 0x00020000;
 // Any offset at or above num_records reads zero / drops the store. A, C and
 // the split-K partials are addressed through windows that start at the
-// tile's first row (rows_at), B through a window that starts at the k-tile's
-// first row (b_window), so only a tile's rows, and a k-tile's rows of B, must
-// span fewer than 2^31 bytes (the host checks a tighter bound).
+// tile's first row (rows_at), so only a tile's rows must span fewer than
+// 2^31 bytes; B is addressed whole (the host checks both).
 static constexpr uint32_t kOob = 0x80000000u;
 // Cache-policy operand of a buffer store that sets nt (non-temporal) on gfx950.
 static constexpr int kStoreNT = 2;
@@ -106,15 +105,6 @@ __device__ __forceinline__ const void *rows_at(const void *p, int row0, int ld, 
 __device__ __forceinline__ uint32_t rows_bytes(int row0, int rows, int ld, int esize) {
   const uint64_t b = (uint64_t)(rows - row0) * (uint64_t)ld * (uint64_t)esize;
   return b < (uint64_t)kOob ? (uint32_t)b : kOob - 16u;
-}
-
-// B's window for the k-tile that starts at row k0: every tile reads B down
-// its whole K, so B's window moves with the k-tile. `bytes` is one k-tile's
-// rows (block_k * ldb * 2; every vector offset a k-tile's load forms lies
-// below it, rows past K being refused by the kernels' own masks), or 0 for an
-// empty window, which loads zeros.
-__device__ __forceinline__ u32x4 b_window(const GemmParams &p, int k0, uint32_t bytes) {
-  return rsrc_dwords(rows_at(p.B, k0, p.ldb, 2), bytes);
 }
 
 // s_waitcnt vmcnt(N) (expcnt / lgkmcnt untouched), gfx9 encoding.
@@ -374,9 +364,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // partial last k-tile (K % 64 = 8r, r = 1..7) a lane's A chunk holds
   // k = 64 kfull + 8 a_lc and loads from kOob unless a_lc < r, and B round l
   // holds k rows 64 kfull + 8l .. +7, so rounds l >= r take a descriptor of
-  // zero records. The buffer range check covers the vector offset only, not
-  // the scalar offset that carries the round and the k-tile, so every such
-  // element is refused here rather than left to the check. Past the edges the
+  // zero records. Every such element is refused here, by its offset or its
+  // descriptor, rather than left to the buffer range check (the window's
+  // records reach the matrix end, not the edge of the problem). Past the edges the
   // ring holds zeros: in M and N they only reach C elements that are not
   // stored, in K they add nothing.
   const int a_row0 = (wave * 64 + lane) >> 3;
@@ -395,10 +385,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
           ? ((uint32_t)b_row0 * (uint32_t)p.ldb + (uint32_t)(n0 + (b_lc ^ 2) * 8)) * 2u
           : kOob;
   const uint32_t a_round = 32u * (uint32_t)p.lda * 2u, b_round = 8u * (uint32_t)p.ldb * 2u;
-  const uint32_t a_ktile = BK * 2u;
-  const uint32_t b_win = BK * 2u * (uint32_t)p.ldb; // one k-tile's rows of B
+  const uint32_t a_ktile = BK * 2u, b_ktile = BK * 2u * (uint32_t)p.ldb;
   const void *a_tile = rows_at(p.A, m0, p.lda, 2); // A's window starts at row m0
   const uint32_t a_bytes = rows_bytes(m0, p.M, p.lda, 2);
+  const uint32_t b_bytes = (uint32_t)p.K * (uint32_t)p.ldb * 2u;
   const uint32_t wlds = lds0 + wave * 1024u;
   const int k_rounds = (p.K - kfull * BK) / 8; // B rounds of the partial k-tile
   const uint32_t a_kmask = a_lc < k_rounds ? 0u : kOob;
@@ -421,7 +411,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
         else
           load_lds16_at<base + B_AT + (L - 8) * 4096u>(
               kpart && L - 8 >= k_rounds ? rb_none : rb, wlds, (L & 1) ? b_voff1 : b_voff0,
-              (L - 8) * b_round); // rb's window starts at k-tile kt's first row
+              (uint32_t)kt * b_ktile + (L - 8) * b_round);
       }
     });
   };
@@ -522,9 +512,9 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 
   // prologue: k-tiles 0 and 1 in flight, wait for 0, run it up to its barrier
   {
-    const u32x4 ra = rsrc_dwords(a_tile, a_bytes), rb = b_window(p, 0, b_win);
+    const u32x4 ra = rsrc_dwords(a_tile, a_bytes), rb = rsrc_dwords(p.B, b_bytes);
     const u32x4 ra1 = rsrc_dwords(a_tile, nk > 1 ? a_bytes : 0u);
-    const u32x4 rb1 = b_window(p, BK, nk > 1 ? b_win : 0u); // k-tile 1, or nothing
+    const u32x4 rb1 = rsrc_dwords(p.B, nk > 1 ? b_bytes : 0u);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
       load(ra, rb, 0, S0{}, l, KM{});
@@ -547,7 +537,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(a_tile, ok ? a_bytes : 0u);
-    const u32x4 rb = b_window(p, (it + 2) * BK, ok ? b_win : 0u); // k-tile it+2, or nothing
+    const u32x4 rb = rsrc_dwords(p.B, ok ? b_bytes : 0u);
     // k-tile it+1 landed (this wave's part), and this wave's reads of stage
     // S are done (the last A rows of k step 1 are read in k step 0 but only
     // consumed after the barrier, by MFMAs 40..63)
@@ -700,6 +690,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
+  const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
+
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
   int prog = blockIdx.x;
@@ -811,10 +803,9 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         const int i = l - LA;
         const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
         const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
-        // B's window starts at the k-tile's first row
-        load_lds16(b_window(p, k0, BK * 2u * (uint32_t)p.ldb), b_lds + i * NW * 1024u,
+        load_lds16(rb4, b_lds + i * NW * 1024u,
                    (kt_ok && krow < p.K) ? b_voff : kOob,
-                   i * T::B_ROWS_PER_LOAD * p.ldb * 2);
+                   (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
       }
     };
     auto issue_tile = [&](int kt, int stage) {
@@ -1308,6 +1299,7 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = wave >= NW;
+  const u32x4 rb4 = rsrc_dwords(p.B, (uint32_t)p.K * (uint32_t)p.ldb * 2u);
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
   int prog = blockIdx.x;
@@ -1366,9 +1358,8 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
           const int i = l - LA;
           const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
           const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
-          // B's window starts at the k-tile's first row
-          load_lds16(b_window(p, k0, BK * 2u * (uint32_t)p.ldb), b_lds + i * NW * 1024u,
-                     (kt_ok && krow < p.K) ? b_voff : kOob, i * T::B_ROWS_PER_LOAD * p.ldb * 2);
+          load_lds16(rb4, b_lds + i * NW * 1024u, (kt_ok && krow < p.K) ? b_voff : kOob,
+                     (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
         }
       };
       auto issue_tile = [&](int kt, int stage) {

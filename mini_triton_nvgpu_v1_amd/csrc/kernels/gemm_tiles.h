@@ -34,12 +34,17 @@
 // Tiles whose plain f32-partial instance (output mode 1: split-K partials and
 // plain f32 C) is built with producer waves (gemm_kernel_pw: as many load-only
 // waves as compute waves), in place of the general loop's build of the same
-// key. Listed where that measured faster: 128x64x64 on 8 waves, 3 stages,
-// the split-K workload's tile (512^2 x 16384 in 8 splits: 18.9 -> 16.8 us
-// per call). The same build on 4 stages, or on 2x2 and 4x1 wave grids, ran
-// 0.2-1.4 us slower per call there. Entries are not separated: each X supplies its own
-// separator.
-#define TBK_PRODUCER_TILES(X) X(128, 64, 64, 4, 2, 3)
+// key. The key serves split-K partials and plain f32 C alike, so a tile is
+// listed where the build measured at least as fast in both (same box,
+// bit-identical results):
+//  * 128x64x64 on 8 waves, 3 stages, the split-K workload's tile: 512^2 x
+//    16384 in 8 splits 18.9 -> 16.8 us per call; 2048^3 plain f32 C equal;
+//  * 64x64x64 on 4 waves, 3 stages: 256^2 x 32768 in 16 splits 16.9 -> 15.0
+//    us per call; 2048^3 plain f32 C 40.6 -> 35.6 us.
+// Not listed: 64x128 (2x4, 2x2) and 128x64 (2x2) gain 5-10% on split-K but
+// lose 12-23% on plain f32 C; 128x128 and 256x64 gain nothing.
+// Entries are not separated: each X supplies its own separator.
+#define TBK_PRODUCER_TILES(X) X(128, 64, 64, 4, 2, 3) X(64, 64, 64, 2, 2, 3)
 
 #define TBK_TILES_64x64(X) \
   X(64, 64, 32, 1, 1, 2), X(64, 64, 32, 1, 1, 3), X(64, 64, 32, 1, 1, 4), \

@@ -144,15 +144,18 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
     return fail("num_programs disagrees with the mapping's launch formula");
 
   // 32-bit buffer offsets: A, C and the split-K partial planes are addressed
-  // through windows that start at each tile's first row, B through windows
-  // that start at each k-tile's first row, so a tile's rows (block_m of A and
-  // C) and a k-tile's rows (block_k of B) must span less than 1 GiB, well
-  // inside the offsets' 2^31 range. The operands' sizes are otherwise free.
+  // through windows that start at each tile's first row, so a tile's rows
+  // (block_m of them) must span less than 1 GiB (well inside the offsets'
+  // 2^31 range); B is addressed whole and must span less than 2 GiB. The
+  // operands' total sizes are otherwise free.
   const int64_t lim = (int64_t)1 << 31, tile_lim = (int64_t)1 << 30;
   if (c.block_m * c.lda * 2 >= tile_lim || c.block_m * c.ldc * 4 >= tile_lim ||
-      c.block_m * c.n * 4 >= tile_lim || c.block_k * c.ldb * 2 >= tile_lim)
-    return fail("a tile's rows of A, B or C span 1 GiB or more (leading dimensions too "
+      c.block_m * c.n * 4 >= tile_lim)
+    return fail("a tile's rows of A or C span 1 GiB or more (leading dimensions too "
                 "large for the 32-bit buffer offsets of this backend)");
+  if (c.k * c.ldb * 2 >= lim)
+    return fail("B larger than 2 GiB is not supported by the 32-bit buffer "
+                "addressing of this backend");
   if (c.m >= lim || c.n >= lim || c.k >= lim)
     return fail("M, N and K must be below 2^31");
   if (total_work > std::numeric_limits<int>::max())

@@ -430,7 +430,9 @@ def test_tb_opt_instance_table_equals_the_kernel_registry():
     assert listed[pw] == ("producer_waves", 6, 3, -1)
     waves = _listed_instances(loader_waves=True)
     assert waves[pw] == 8
-    assert {n for n, v in waves.items() if v} == {pw}
+    pw64 = "tb_gemm_gfx950_64x64x64_w2x2_s3_out1"
+    assert listed[pw64][0] == "producer_waves" and waves[pw64] == 4
+    assert {n for n, v in waves.items() if v} == {pw, pw64}
     assert listed["tb_gemm_gfx950_128x64x64_w4x2_s3_out0"] == ("burst", 6, 3, -1)
     L = tb.lib()
     import ctypes
@@ -531,11 +533,12 @@ def test_no_plan_legal_configuration_lacks_a_kernel(bm, bn):
 
 
 def test_plan_over_operands_past_2gib():
-    """The plan pipeline and the C ABI bind operands of several GiB (A and B
-    past 2 GiB each): the kernels address them in per-tile windows."""
-    w = configs.Workload("big", 139264, 4096, 270336, 1, 0, (256, 256, 64), num_waves=4)
+    """The plan pipeline and the C ABI bind A and C of several GiB: the
+    kernels address them in per-tile windows. B stays under 2 GiB."""
+    w = configs.Workload("big", 262144, 32768, 8192, 1, 0, (256, 256, 64), num_waves=4)
     desc = tb.plan_from_mlir(w.mlir())
     assert desc.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
     cfg = desc.config
-    assert (cfg.m, cfg.n, cfg.k) == (139264, 4096, 270336)
-    assert cfg.m * cfg.lda * 2 > 1 << 31 and cfg.k * cfg.ldb * 2 > 1 << 31
+    assert (cfg.m, cfg.n, cfg.k) == (262144, 32768, 8192)
+    assert cfg.m * cfg.lda * 2 > 1 << 31 and cfg.m * cfg.ldc * 2 > 1 << 31
+    assert cfg.k * cfg.ldb * 2 < 1 << 31
