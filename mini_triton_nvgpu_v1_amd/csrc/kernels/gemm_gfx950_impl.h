@@ -316,15 +316,17 @@ __device__ __forceinline__ void sched_step() {
 // formed as C^T += B^T A^T, so lane l ends with C[16ii + l%16][16jj + 4(l/16)
 // + r], r = 0..3. Slot schedule per 32-deep k step (64 MFMAs, m = 8ii + jj):
 // the reads of the next k step in the order A0, B0 (two halves) .. B7, A1 ..
-// A7, op o in slot 8o/3; the barrier before slot 16 of the last k step; after
-// it the next k-tile's first reads (op o in slot 16 + 2o) and its refill, one
-// load every 5 slots (loads 0..9 in slots 16..61, 10..15 in slots 2..27 of
+// A7, op o in slot 8o/3; the barrier before slot 8 of the last k step; after
+// it the next k-tile's first reads (op o in slot 8 + 7o/3) and its refill, one
+// load every 5 slots (loads 0..11 in slots 8..63, 12..15 in slots 4..19 of
 // the next k-tile): a CU then asks the L2 for 64 KiB over ~1200 cycles, about
 // what the L2 -> CU path sustains. Bunched into 40 slots, the queued loads
 // held up the lone wave's issue (1% slower); every 4 or 3 slots measured
 // 0.7% and 1.3% slower than every 5. With the barrier at slot 40 and the
 // next k-tile's reads one per slot after it, the k-tile ran 27 cycles (1.2%)
-// longer: a lone wave pays for LDS instructions issued back to back.
+// longer: a lone wave pays for LDS instructions issued back to back; the
+// reads spread over the 56 slots after a barrier at slot 8 ran 0.3% faster
+// than over the 48 after one at slot 16.
 // s_waitcnt depths of the 16x16x32 instance: the prologue issues k-tiles 0
 // and 1 whole (16 loads each per lane) and waits for k-tile 0; each
 // barrier waits for every load and LDS read of the wave.

@@ -24,8 +24,8 @@
 
 namespace tbk {
 
-template <int BQ_ = 16, int RNUM = 8, int RDEN = 3, int ACC_WAITS = 24, int R1NUM = 2,
-          int R1DEN = 1>
+template <int BQ_ = 8, int RNUM = 8, int RDEN = 3, int ACC_WAITS = 24, int R1NUM = 7,
+          int R1DEN = 3>
 struct Mfma16Schedule {
   static constexpr int NSLOT = 64;  // MFMAs per 32-deep k step: 8 x 8 tiles of 16 x 16
   static constexpr int NREAD = 24;  // fragment reads per k step: A0, B0 (2 halves) .. B7, A1 .. A7
