@@ -12,7 +12,8 @@ cores, on a bounded sample of the same workload).
 Timing: a clock-settle phase (--settle-s seconds of launches), W warm-up
 launches, then --rounds rounds of exactly K launches, each bracketed by a
 device synchronize; `value` and `ms_per_step` are the median round. The
-timed output is checked against torch.matmul in f32 on every 16th row.
+timed output is checked against torch.matmul in f32 on every 16th row (for
+f32 C += A*B, one more launch on the prior C after the timed rounds).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--rounds R]
        [--settle-s S] [--no-extra] [--no-cpu] [--workload NAME]
@@ -58,10 +59,17 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
     desc = tb.plan_from_mlir(w.mlir())
     A = torch.empty((w.M, w.K), dtype=torch.float16, device=device)
     B = torch.empty((w.K, w.N), dtype=torch.float16, device=device)
-    C = torch.empty((w.M, w.N), dtype=torch.float16, device=device)
+    C = torch.empty((w.M, w.N), dtype=torch.float32 if w.c_f32 else torch.float16,
+                    device=device)
     ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=device)
           if desc.workspace_bytes else None)
     stream = torch.cuda.current_stream(device)
+    C0 = None
+    if w.c_f32:  # C += A*B: a seeded prior C, uniform in [-1, 1)
+        C0 = torch.empty((w.M, w.N), dtype=torch.float16, device=device)
+        tb.fill_seeded_f16(C0, w.M, w.N, w.seed ^ 0xC0, 0, 1.0, stream=stream)
+        C0 = C0.float()
+        C.copy_(C0)
     bias = None
     if w.bias:  # fused bias step: N seeded values
         bias = torch.empty((1, w.N), dtype=torch.float16, device=device)
@@ -93,20 +101,29 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
         torch.cuda.synchronize(device)
         walls.append(time.perf_counter() - t0)
         events.append(region[0].elapsed_time(region[1]) / steps)
-    ok = verify_output(w, A, B, C, bias)
+    if C0 is not None:
+        # the timed launches accumulated into C: check one more launch on the
+        # prior C instead
+        C.copy_(C0)
+        launch()
+        torch.cuda.synchronize(device)
+    ok = verify_output(w, A, B, C, bias, C0)
     return {"wall_s": statistics.median(walls), "avg_launch_ms": statistics.median(events),
             "round_wall_s": walls, "round_launch_ms": events, "kernel": desc.kernel_name,
             "settle_launches": settle_launches, "verified": ok}
 
 
-def verify_output(w, A, B, C, bias):
+def verify_output(w, A, B, C, bias, C0=None):
     """The timed launches' output against torch.matmul in f32 on the same
-    device buffers (an independent GEMM), with the fused steps applied, on
-    every 16th row: per-element |err| <= 1e-2 (|ref| + 1)."""
+    device buffers (an independent GEMM), plus the prior C for C += A*B, with
+    the fused steps applied, on every 16th row: per-element
+    |err| <= 1e-2 (|ref| + 1)."""
     import torch
 
     rows = torch.arange(0, w.M, 16, device=A.device)
     ref = A[rows].float() @ B.float()
+    if C0 is not None:
+        ref += C0[rows]
     if bias is not None:
         ref += bias.float().view(1, -1)
     if w.activation == "relu":
@@ -250,7 +267,7 @@ def main() -> int:
 
     extra = {}
     if not args.no_extra:
-        for other in configs.ALL + configs.FUSED:
+        for other in configs.ALL + configs.FUSED + configs.F32_ACCUMULATE:
             if other.name == w.name:
                 continue
             # a few tens of ms of GPU time per extra: long enough for a steady clock
@@ -293,7 +310,8 @@ def main() -> int:
         "config": {"workload": w.name, "M": w.M, "N": w.N, "K": w.K,
                    "tile": list(w.block), "num_waves": w.num_waves,
                    "group_m": w.group_m, "split_k": w.split_k,
-                   "persistent": w.persistent, "c_dtype": "f16",
+                   "persistent": w.persistent,
+                   "c_dtype": "f32 (C += A*B)" if w.c_f32 else "f16",
                    "accumulate": "f32", "kernel": r["kernel"],
                    "plan_pipeline_ms": round(plan_time_ms(w), 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3),

@@ -65,9 +65,9 @@ extern "C" {
 
 /* MFMA instruction of the instance (reference MmaKind,
  * include/tb/Analysis/KernelConfig.h:18-20, which names the mma.sync shape).
- * 16x16x32 exists for the 4-wave 256x256x64 2-stage f16 tile, any M, N and
- * K (tile, grouped or persistent order; no split-K): the plan selects it
- * there. */
+ * 16x16x32 exists for the 4-wave 256x256x64 2-stage tile with an f16 C, a
+ * plain f32 C or f32 C += A*B, any M, N and K (tile, grouped or persistent
+ * order; no split-K): the plan selects it there. */
 #define TB_MFMA_32X32X16 0 /* v_mfma_f32_32x32x16_f16 */
 #define TB_MFMA_16X16X32 1 /* v_mfma_f32_16x16x32_f16 */
 

@@ -14,8 +14,8 @@ import dataclasses
 import math
 from dataclasses import dataclass, field
 
-from . import (ACC_INIT_ZERO, ACT_GELU_TANH, ACT_NONE, ACT_RELU, ACT_SILU,
-               CLAMP_MAX, CLAMP_MIN, DTYPE_F16, EPI_BIAS_F16, EPI_BIAS_F32,
+from . import (ACC_INIT_LOAD_C, ACC_INIT_ZERO, ACT_GELU_TANH, ACT_NONE, ACT_RELU, ACT_SILU,
+               CLAMP_MAX, CLAMP_MIN, DTYPE_F16, DTYPE_F32, EPI_BIAS_F16, EPI_BIAS_F32,
                EPI_BIAS_NONE, MAP_GROUPED_TILE, MAP_PERSISTENT_GROUPED,
                MAP_SPLIT_K, MAP_TILE, MFMA_16X16X32, MFMA_32X32X16, RED_NONE,
                RED_WORKSPACE, GemmConfig)
@@ -73,6 +73,9 @@ class Workload:
     activation: str = ""    # "", "relu", "gelu_tanh" or "silu"
     clamp_min: float | None = None
     clamp_max: float | None = None
+    # f32 C with C += A*B (the reference's own tb.matmul semantics) instead of
+    # f16 C = A*B
+    c_f32: bool = False
 
     @property
     def flop(self) -> int:
@@ -80,8 +83,10 @@ class Workload:
 
     @property
     def algo_bytes(self) -> int:
-        """Algorithmic HBM bytes: A, B and the f16 C each moved once."""
-        return 2 * (self.M * self.K + self.K * self.N + self.M * self.N)
+        """Algorithmic HBM bytes: A and B moved once, and the f16 C written
+        once (an f32 C += A*B: read and written once)."""
+        c_bytes = 8 * self.M * self.N if self.c_f32 else 2 * self.M * self.N
+        return 2 * (self.M * self.K + self.K * self.N) + c_bytes
 
     @property
     def scale(self) -> float:
@@ -91,8 +96,10 @@ class Workload:
     def seed_b(self) -> int:
         return self.seed ^ 0xB
 
-    def mlir(self, c_type: str = "f16") -> str:
-        """The tb.matmul module fed to the plan pipeline."""
+    def mlir(self, c_type: str | None = None) -> str:
+        """The tb.matmul module fed to the plan pipeline (an f32 C makes it
+        C += A*B)."""
+        c_type = c_type or ("f32" if self.c_f32 else "f16")
         attrs = {"tb.num-warps": f"{self.num_waves} : i64",
                  "tb.requested-stages": f"{self.stages} : i64"}
         if self.split_k > 1:
@@ -149,7 +156,8 @@ class Workload:
             programs = tiles_m * tiles_n
         return GemmConfig(
             m=self.M, n=self.N, k=self.K, lda=self.K, ldb=self.N, ldc=self.N,
-            c_dtype=DTYPE_F16, acc_init=ACC_INIT_ZERO, block_m=bm, block_n=bn,
+            c_dtype=DTYPE_F32 if self.c_f32 else DTYPE_F16,
+            acc_init=ACC_INIT_LOAD_C if self.c_f32 else ACC_INIT_ZERO, block_m=bm, block_n=bn,
             block_k=bk, num_waves=self.num_waves, wave_grid_m=wg[0],
             wave_grid_n=wg[1], stages=self.stages, mapping=mapping,
             group_m=self.group_m if mapping not in (MAP_TILE, MAP_SPLIT_K) else 1,
@@ -168,7 +176,7 @@ class Workload:
 
     def mfma16_supported(self) -> bool:
         """The plan's choice of v_mfma_f32_16x16x32_f16: the 4-wave
-        256x256x64 2-stage f16 tile, any M, N and K, no split-K."""
+        256x256x64 2-stage tile (f16 or f32 C), any M, N and K, no split-K."""
         return (self.block == (256, 256, 64) and self.num_waves == 4 and self.stages == 2
                 and self.split_k == 1)
 
@@ -201,4 +209,8 @@ ALL = [SMOKE, RAGGED, RAGGED_128, ROOFLINE, SPLIT_K, PERSISTENT]
 # on the f32 result before the f16 store): what the fusion costs.
 FUSED = [dataclasses.replace(ROOFLINE, name="gemm_4096_bias_gelu", bias="f16",
                              activation="gelu_tanh")]
-BY_NAME = {w.name: w for w in ALL + FUSED}
+# The roofline GEMM in the reference's own semantics: f32 C += A*B (the
+# prior C read, the sum written back as f32).
+F32_ACCUMULATE = [dataclasses.replace(ROOFLINE, name="gemm_4096_f32_accumulate",
+                                      c_f32=True)]
+BY_NAME = {w.name: w for w in ALL + FUSED + F32_ACCUMULATE}

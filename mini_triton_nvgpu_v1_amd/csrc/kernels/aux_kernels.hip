@@ -161,13 +161,15 @@ hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
 }
 
 // ---- instance registry ----------------------------------------------------
-// One table per shape and flavour (gemm_inst.hip) plus the 16x16x32 tables.
+// One table per shape and flavour (gemm_inst.hip) plus the 16x16x32 tables
+// (f16 C; f32 C).
 #define TBK_DECLARE(SHAPE)                                                      \
   const KernelEntry *entries_##SHAPE(int *n);                                  \
   const KernelEntry *entries_##SHAPE##_epi(int *n);
 TBK_SHAPES(TBK_DECLARE)
 #undef TBK_DECLARE
 const KernelEntry *entries_mfma16(int *n);
+const KernelEntry *entries_mfma16_f32(int *n);
 const KernelEntry *entries_producer(int *n);
 
 static bool same_key(const KernelKey &a, const KernelKey &b) {
@@ -188,8 +190,8 @@ static const KernelEntry *preferred(const KernelEntry *e) {
 }
 
 #define TBK_TABLES(SHAPE) entries_##SHAPE, entries_##SHAPE##_epi,
-static const KernelEntry *(*const kTables[])(int *) = {TBK_SHAPES(TBK_TABLES)
-                                                           entries_mfma16};
+static const KernelEntry *(*const kTables[])(int *) = {
+    TBK_SHAPES(TBK_TABLES) entries_mfma16, entries_mfma16_f32};
 #undef TBK_TABLES
 
 int kernel_count() {

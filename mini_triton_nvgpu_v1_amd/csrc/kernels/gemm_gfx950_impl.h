@@ -335,8 +335,12 @@ constexpr int kMfma16VmPrologue = kMfma16LoadsPerThread;
 constexpr int kMfma16VmLoop = 0;
 constexpr int kMfma16LgkmLoop = 0;
 
-template <bool EPI, bool KPART>
+// OUT: kOutF16 (f16 C), kOutF32Partial (a plain f32 C store: never split-K
+// here) or kOutF32Accum (f32 C += A*B); the main loop is the same for all.
+template <int OUT, bool EPI, bool KPART>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
+  static_assert(OUT == kOutF16 || OUT == kOutF32Partial || OUT == kOutF32Accum,
+                "no atomic or split-K output on the 16x16x32 instance");
   // slots, read placement and hazard rules: Mfma16Schedule (compile-time
   // checked)
   using Sched = Mfma16Schedule<>;
@@ -602,76 +606,157 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   int el = lane;
   asm volatile("" : "+v"(el));
   const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
-  epi_f32x4 bv[EPI ? 8 : 1];
-  if constexpr (EPI) { // every bias load first: one memory latency
-    const int ccol = n0 + wn * 128 + 4 * (el >> 4);
+  if constexpr (OUT == kOutF16) {
+    epi_f32x4 bv[EPI ? 8 : 1];
+    if constexpr (EPI) { // every bias load first: one memory latency
+      const int ccol = n0 + wn * 128 + 4 * (el >> 4);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      bv[j] = epi_load_bias(ea, ccol + 16 * j, p.N);
-  }
-  barrier(); // every wave is past its last fragment read and load
-  TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
-  // clamp bounds: -inf / +inf for a clamp that is off
-  const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
-  const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
-  // C's window starts at row m0
-  const __amdgpu_buffer_rsrc_t rc =
-      make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
-  const int q = el & 15;
-  // One 16-row block of the wave tile at a time: its 8 tiles go into LDS,
-  // then its 16 rows come back and go out, so the stores of block i run
-  // while block i+1's conversions (and fused steps) execute. The region is
-  // this wave's alone and a wave's LDS operations complete in order, so no
-  // barrier separates a block's writes from its reads.
-  auto epilogue = [&](auto act_c, auto clamp_c) {
-    constexpr int ACT = decltype(act_c)::value;
-    constexpr bool CLAMP = decltype(clamp_c)::value;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 16 * i + (el & 15);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float x[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[e] = acc[i][j][e];
-          if constexpr (EPI)
-            x[e] = epi_apply_t<ACT, CLAMP>(x[e], bv[j][e], lo, hi);
-        }
-        u32x2 v;
-        v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
-        v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
-               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
-        const int chunk = (2 * j + (el >> 5)) ^ (r & 7);
-        const int half = ((el >> 4) & 1) ^ ((r >> 3) & 1);
-        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
-        if (j & 1)
-          __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int t = 4 * i; t < 4 * i + 4; ++t) {
-        const int rr = t * 4 + (el >> 4); // rows 16i .. 16i+15
-        u32x4 v = *(const TBK_LDS u32x4 *)(wl + rr * 256 + ((q ^ (rr & 7)) * 16));
-        if ((rr >> 3) & 1)
-          v = (u32x4){v[2], v[3], v[0], v[1]};
-        const int row = m0 + wm * 128 + rr, col = n0 + wn * 128 + 8 * q;
-        const uint32_t off =
-            row < p.M && col < p.N
-                ? ((uint32_t)(wm * 128 + rr) * (uint32_t)p.ldc + (uint32_t)col) * 2u
-                : kOob;
-        // non-temporal (nt): C is written once and not read again by this
-        // kernel; measured 0.7% faster at 4096^3 than the default policy
-        __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < 8; ++j)
+        bv[j] = epi_load_bias(ea, ccol + 16 * j, p.N);
     }
-  };
-  // the activation and clamp are dispatched once, not per element
-  if constexpr (EPI)
-    epi_dispatch(p.epi_act, p.epi_clamp, epilogue);
-  else
-    epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+    barrier(); // every wave is past its last fragment read and load
+    TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
+    // clamp bounds: -inf / +inf for a clamp that is off
+    const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
+    const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
+    // C's window starts at row m0
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
+    const int q = el & 15;
+    // One 16-row block of the wave tile at a time: its 8 tiles go into LDS,
+    // then its 16 rows come back and go out, so the stores of block i run
+    // while block i+1's conversions (and fused steps) execute. The region is
+    // this wave's alone and a wave's LDS operations complete in order, so no
+    // barrier separates a block's writes from its reads.
+    auto epilogue = [&](auto act_c, auto clamp_c) {
+      constexpr int ACT = decltype(act_c)::value;
+      constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 16 * i + (el & 15);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float x[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[e] = acc[i][j][e];
+            if constexpr (EPI)
+              x[e] = epi_apply_t<ACT, CLAMP>(x[e], bv[j][e], lo, hi);
+          }
+          u32x2 v;
+          v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
+          v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
+          const int chunk = (2 * j + (el >> 5)) ^ (r & 7);
+          const int half = ((el >> 4) & 1) ^ ((r >> 3) & 1);
+          *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+          if (j & 1)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 4 * i; t < 4 * i + 4; ++t) {
+          const int rr = t * 4 + (el >> 4); // rows 16i .. 16i+15
+          u32x4 v = *(const TBK_LDS u32x4 *)(wl + rr * 256 + ((q ^ (rr & 7)) * 16));
+          if ((rr >> 3) & 1)
+            v = (u32x4){v[2], v[3], v[0], v[1]};
+          const int row = m0 + wm * 128 + rr, col = n0 + wn * 128 + 8 * q;
+          const uint32_t off =
+              row < p.M && col < p.N
+                  ? ((uint32_t)(wm * 128 + rr) * (uint32_t)p.ldc + (uint32_t)col) * 2u
+                  : kOob;
+          // non-temporal (nt): C is written once and not read again by this
+          // kernel; measured 0.7% faster at 4096^3 than the default policy
+          __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    // the activation and clamp are dispatched once, not per element
+    if constexpr (EPI)
+      epi_dispatch(p.epi_act, p.epi_clamp, epilogue);
+    else
+      epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+  } else {
+    // f32 C through LDS, one 16-row block of the wave tile at a time. Lane l
+    // holds row 16i + l%16, columns 16j + 4(l/16) .. +3 of block i (16 bytes
+    // per 16x16 tile j); they go to LDS as 512-byte rows, chunk c = 4j + l/16
+    // of row r at c ^ r (a quarter wave's 16 rows land in 16 different 16-byte
+    // bank groups), and come back as 2 whole rows per ds_read_b128 / buffer
+    // store. Blocks rotate over four 8 KiB regions of the wave's 32 KiB: a
+    // wave's LDS operations complete in order, so block i+4's writes never
+    // overtake block i's reads. C += A*B reads the prior C as the same whole
+    // rows, PF blocks ahead of the block being stored, and adds it to the sum
+    // before the fused steps (the general loop's order: epilogue(C + acc)).
+    constexpr int PF = EPI ? 2 : 4; // 4 blocks (128 VGPRs) spill with the fused steps
+    const int q = el & 31, hr = el >> 5; // a lane's 16-byte chunk and row parity
+    const int col = n0 + wn * 128 + 4 * q;
+    // C's window starts at row m0
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
+    auto c_off = [&](int i, int t) -> uint32_t {
+      const int rr = wm * 128 + 16 * i + 2 * t + hr; // row of the tile
+      return m0 + rr < p.M && col < p.N
+                 ? ((uint32_t)rr * (uint32_t)p.ldc + (uint32_t)col) * 4u
+                 : kOob;
+    };
+    f32x4 old[OUT == kOutF32Accum ? PF : 1][8];
+    auto load_old = [&](int i) {
+      if constexpr (OUT == kOutF32Accum) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          old[i % PF][t] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, c_off(i, t), 0, 0));
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+      load_old(i);
+    const epi_f32x4 bias = EPI ? epi_load_bias(ea, col, p.N) : epi_f32x4{};
+    barrier(); // every wave is past its last fragment read and load
+    TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
+    const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
+    const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
+    auto epilogue = [&](auto act_c, auto clamp_c) {
+      constexpr int ACT = decltype(act_c)::value;
+      constexpr bool CLAMP = decltype(clamp_c)::value;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        TBK_LDS char *blk = wl + (i & 3) * 8192;
+        const int r = el & 15, g = el >> 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          *(TBK_LDS f32x4 *)(blk + r * 512 + (((4 * j + g) ^ r) * 16)) = acc[i][j];
+          if (j & 1)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int rr = 2 * t + hr;
+          f32x4 v = *(const TBK_LDS f32x4 *)(blk + rr * 512 + ((q ^ rr) * 16));
+          if constexpr (OUT == kOutF32Accum)
+            v += old[i % PF][t];
+          if constexpr (EPI) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[e] = epi_apply_t<ACT, CLAMP>(v[e], bias[e], lo, hi);
+          }
+          // a plain f32 C is written once and not read again by this kernel
+          // (non-temporal); C += A*B keeps the default policy
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc,
+                                                 c_off(i, t), 0,
+                                                 OUT == kOutF32Partial ? kStoreNT : 0);
+        }
+        if (i + PF < 8)
+          load_old(i + PF);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if constexpr (EPI)
+      epi_dispatch(p.epi_act, p.epi_clamp, epilogue);
+    else
+      epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+  }
 }
 
 // EPI: the fused epilogue steps (bias, activation, clamp) are compiled in.
@@ -1504,11 +1589,10 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
   }
 }
 
-// The 16x16x32 instance of the 4-wave 256x256x64 2-stage f16 configuration
-// (any M, N and K; tile, grouped or persistent order).
-template <bool EPI, bool KPART>
-__global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
-  __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
+// The programs of the 16x16x32 instance of the 4-wave 256x256x64 2-stage
+// configuration (any M, N and K; tile, grouped or persistent order).
+template <int OUT, bool EPI, bool KPART>
+__device__ __forceinline__ void mfma16_programs(const GemmParams &p, u32x4 *lds) {
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
   int prog = blockIdx.x;
@@ -1521,8 +1605,22 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
     map_program(p, work, tile_m, tile_n, part);
     if (work != prog)
       __syncthreads(); // every wave read its staged epilogue back
-    mfma16_tile<EPI, KPART>(p, tile_m * 256, tile_n * 256, lds);
+    mfma16_tile<OUT, EPI, KPART>(p, tile_m * 256, tile_n * 256, lds);
   }
+}
+
+// f16 C
+template <bool EPI, bool KPART>
+__global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
+  __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
+  mfma16_programs<kOutF16, EPI, KPART>(p, lds);
+}
+
+// f32 C: a plain store (OUT = kOutF32Partial) or C += A*B (kOutF32Accum)
+template <int OUT, bool EPI, bool KPART>
+__global__ __launch_bounds__(256, 1) void gemm_mfma16_f32(GemmParams p) {
+  __shared__ u32x4 lds[8192];
+  mfma16_programs<OUT, EPI, KPART>(p, lds);
 }
 
 } // namespace tbk

@@ -37,8 +37,10 @@ const std::vector<InstanceKey> &gfx950Instances() {
       for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
         v.push_back({t.bm, t.bn, t.bk, t.wgm, t.wgn, out, t.stages, 1, TB_MFMA_32X32X16});
     }
-    for (int epi = 0; epi <= 1; ++epi)
-      v.push_back({256, 256, 64, 2, 2, kInstOutF16, 2, epi, TB_MFMA_16X16X32});
+    // 16x16x32: f16 C, plain f32 C and f32 C += A*B (no split-K)
+    for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
+      for (int epi = 0; epi <= 1; ++epi)
+        v.push_back({256, 256, 64, 2, 2, out, 2, epi, TB_MFMA_16X16X32});
     return v;
   }();
   return all;

@@ -157,14 +157,15 @@ static int64_t opI64(const Op &op, const char *name, bool required, int64_t dflt
   return it->second->i;
 }
 
-// gfx950: the v_mfma_f32_16x16x32_f16 instance exists for the 4-wave
-// 256x256x64 2-stage tile with f16 C (the plan's 2x2 wave grid of 128x128
-// wave tiles), any M, N and K (it masks ragged edges). Per FLOP it moves a
-// quarter of the accumulator register traffic of 32x32x16, which this
-// power-limited part turns into a higher sustained clock.
+// gfx950: the v_mfma_f32_16x16x32_f16 instances exist for the 4-wave
+// 256x256x64 2-stage tile (the plan's 2x2 wave grid of 128x128 wave tiles)
+// with an f16 C, a plain f32 C or f32 C += A*B, any M, N and K (they mask
+// ragged edges). Per FLOP it moves a quarter of the accumulator register
+// traffic of 32x32x16, which this power-limited part turns into a higher
+// sustained clock. (Split-K has no 16x16x32 instance: the caller checks.)
 bool mfma16x16x32Supported(const KernelConfig &c) {
   return c.blockM == 256 && c.blockN == 256 && c.blockK == 64 && c.numWarps == 4 &&
-         c.requestedStages == 2 && c.cScalar == ScalarKind::F16;
+         c.requestedStages == 2;
 }
 
 // Reference: KernelConfig.cpp:86-132 (tb.matmul) and the post-cleanup
@@ -273,7 +274,7 @@ void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t) {
                 "`mfma_f32_16x16x32_f16`");
   if (c.mmaKind == MmaKind::Mfma16x16x32F16 && !mfma16x16x32Supported(c))
     throw Error("mma = `mfma_f32_16x16x32_f16` is implemented for the 4-wave "
-                "256x256x64 2-stage tile with f16 C only");
+                "256x256x64 2-stage tile only");
   if (c.problemM <= 0 || c.problemN <= 0 || c.problemK <= 0)
     throw Error("problem M/N/K must be positive");
   if (c.blockM <= 0 || c.blockN <= 0 || c.blockK <= 0)

@@ -45,7 +45,8 @@ def main() -> int:
     desc = tb.plan_from_mlir(w.mlir())
     A = torch.empty((w.M, w.K), dtype=torch.float16, device=dev)
     B = torch.empty((w.K, w.N), dtype=torch.float16, device=dev)
-    C = torch.empty((w.M, w.N), dtype=torch.float16, device=dev)
+    C = torch.zeros((w.M, w.N), dtype=torch.float32 if w.c_f32 else torch.float16,
+                    device=dev)
     ws = (torch.empty(desc.workspace_bytes, dtype=torch.uint8, device=dev)
           if desc.workspace_bytes else None)
     tb.fill_seeded_f16(A, w.M, w.K, w.seed, w.dist, w.scale, stream=stream)
@@ -60,7 +61,7 @@ def main() -> int:
         desc.launch(A, B, C, ws, stream=stream, bias=bias)
     torch.cuda.synchronize()
     print(f"profiling: {args.reps} launches of {desc.kernel_name} ({w.name})", flush=True)
-    if args.hipblaslt:
+    if args.hipblaslt and not w.c_f32:
         # the vendor library on the same operands, for side-by-side counters
         for _ in range(args.reps):
             torch.matmul(A, B, out=C)

@@ -54,6 +54,9 @@ def test_kernel_registry_names():
     assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0" in names
     assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32" in names
     assert "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32_epi" in names
+    for out in (1, 2):  # f32 C: plain store, C += A*B
+        for suffix in ("", "_epi"):
+            assert f"tb_gemm_gfx950_256x256x64_w2x2_s2_out{out}_16x16x32{suffix}" in names
 
 
 def _wide(**kw):
@@ -73,6 +76,11 @@ def test_mfma_16x16x32_instance_selection():
     assert d32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
     fused = tb.GemmDesc.from_config(_wide(epi_activation=tb.ACT_RELU))
     assert fused.kernel_name.endswith("_16x16x32_epi")
+    plain32 = tb.GemmDesc.from_config(_wide(c_dtype=tb.DTYPE_F32))
+    assert plain32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out1_16x16x32"
+    accum = tb.GemmDesc.from_config(_wide(c_dtype=tb.DTYPE_F32,
+                                          acc_init=tb.ACC_INIT_LOAD_C))
+    assert accum.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out2_16x16x32"
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -80,7 +88,8 @@ def test_mfma_16x16x32_instance_selection():
     (dict(mapping=tb.MAP_SPLIT_K, split_k=2, reduction=tb.RED_WORKSPACE,
           num_programs=512), "no split-K"),
     (dict(stages=3), "no gfx950 kernel instance.*16x16x32"),
-    (dict(c_dtype=tb.DTYPE_F32), "no gfx950 kernel instance.*16x16x32"),
+    (dict(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_LOAD_C, mapping=tb.MAP_SPLIT_K,
+          split_k=2, reduction=tb.RED_ATOMIC, num_programs=512), "no split-K"),
 ])
 def test_mfma_16x16x32_validation(kw, msg):
     with pytest.raises(tb.TbError, match=msg):

@@ -258,7 +258,8 @@ def test_every_instance(inst, device):
                             mapping=tb.MAP_GROUPED_TILE, split_k=1,
                             reduction=tb.RED_NONE, num_programs=tm * tn, **kw)
         c_dtype = torch.float16
-    elif out == 1 and epi:  # plain f32 store (only fused instances are bound)
+    elif out == 1 and (epi or mfma16):  # plain f32 store (fused instances, and
+        # 16x16x32, which has no split-K)
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_ZERO,
                             mapping=tb.MAP_TILE, split_k=1, reduction=tb.RED_NONE,
                             num_programs=tm * tn, **kw)

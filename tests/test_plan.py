@@ -75,7 +75,7 @@ def test_print_parse_roundtrip(w):
     assert tb_opt(lowered).stdout == lowered
 
 
-@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+@pytest.mark.parametrize("w", configs.ALL + configs.F32_ACCUMULATE, ids=lambda w: w.name)
 def test_plan_config_matches_direct_config(w):
     plan = tb.plan_from_mlir(w.mlir()).config
     direct = w.direct_config()
@@ -83,7 +83,7 @@ def test_plan_config_matches_direct_config(w):
         assert getattr(plan, f) == getattr(direct, f), f
 
 
-@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+@pytest.mark.parametrize("w", configs.ALL + configs.F32_ACCUMULATE, ids=lambda w: w.name)
 def test_lowering_names_the_bound_kernel(w, tmp_path):
     lowered = tb_opt(w.mlir(), f"--pass-pipeline={FULL}").stdout
     name = re.search(r'kernel = "([^"]+)"', lowered).group(1)
@@ -192,16 +192,22 @@ def test_plan_from_mlir_diagnostics(name, text, arg, msg):
 
 def test_mfma_instruction_choice():
     """Without an `mma` attribute the plan takes 16x16x32 exactly where that
-    instance exists: the 4-wave 256x256x64 2-stage f16 tile (M, N and K may
-    be ragged) without split-K. The EncodingPlan records the instruction shape."""
+    instance exists: the 4-wave 256x256x64 2-stage tile with an f16 C or an
+    f32 C (C += A*B, the reference's semantics), M, N and K possibly ragged,
+    without split-K. The EncodingPlan records the instruction shape."""
     def launch(text):
         return tb.plan_from_mlir(text)
     wide = dict(M=512, N=768, K=192, bm=256, bn=256, bk=64)
     assert launch(matmul_module(**wide)).config.mfma == tb.MFMA_16X16X32
-    for kw in (dict(wide, M=520, N=200, exact=False), dict(wide, K=200, exact=False)):
+    for kw in (dict(wide, M=520, N=200, exact=False), dict(wide, K=200, exact=False),
+               dict(wide, c="f32"), dict(wide, c="f32", M=520, K=200, exact=False)):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_16X16X32, kw
-    for kw in (dict(wide, warps=8), dict(wide, bk=32), dict(wide, c="f32"),
+    f32 = tb.plan_from_mlir(matmul_module(**dict(wide, c="f32")))
+    assert f32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out2_16x16x32"
+    for kw in (dict(wide, warps=8), dict(wide, bk=32),
                dict(wide, extra_module=', "tb.split-k" = 3 : i64'),
+               dict(wide, c="f32", extra_module=', "tb.split-k" = 2 : i64, '
+                    '"tb.reduction-mode" = "split_k_parallel"'),
                dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"'), {}):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_32X32X16, kw
     text = tb_opt(matmul_module(**wide), f"--pass-pipeline={MAINLINE}").stdout
@@ -456,7 +462,7 @@ def _async_waits(text):
     return issue, lpt, tail, waits
 
 
-@pytest.mark.parametrize("w", configs.ALL, ids=lambda w: w.name)
+@pytest.mark.parametrize("w", configs.ALL + configs.F32_ACCUMULATE, ids=lambda w: w.name)
 def test_async_plan_states_the_bound_kernels_waits(w):
     """The AsyncPlan's waits are those compiled into the kernel the plan
     binds: vmcnt at the prologue (k group 0), vmcnt at every later barrier,
