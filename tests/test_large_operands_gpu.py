@@ -10,7 +10,7 @@ fp64 oracle, together with the first and last rows:
 * A of 2.1 GiB through the 16x16x32 instance, the general loop and the
   producer-wave split-K build;
 * f16 C of 2.1 GiB (16x16x32 instance), f32 C of 2.1 GiB as a plain store and
-  as C += A*B (general loop);
+  as C += A*B (general loop), and as C += A*B on the 16x16x32 instance;
 * a split-K workspace of 2.3 GiB (eight partial planes), producer-wave build.
 
 Operands are filled on the device with the oracle's SplitMix64 stream (the
@@ -66,6 +66,8 @@ CASES = {
                     tb.ACC_INIT_ZERO, 1, tb.MFMA_32X32X16, "C"),
     "C32_accumulate": (70016, 8192, 64, (128, 128, 64), 4, (2, 2), 2, tb.DTYPE_F32,
                        tb.ACC_INIT_LOAD_C, 1, tb.MFMA_32X32X16, "C"),
+    "C32_accumulate_16x16x32": (70016, 8192, 64, (256, 256, 64), 4, (2, 2), 2, tb.DTYPE_F32,
+                                tb.ACC_INIT_LOAD_C, 1, tb.MFMA_16X16X32, "C"),
     "workspace_producer": (16384, 4608, 1024, (128, 64, 64), 8, (4, 2), 3, tb.DTYPE_F16,
                            tb.ACC_INIT_ZERO, 8, tb.MFMA_32X32X16, "ws"),
 }
