@@ -349,3 +349,40 @@ def test_second_swizzle_term_bijection_and_bank_conflicts():
             assert got == chunk ^ (4 * (k % 4)) ^ (2 * ((k // 8) % 2))
     assert _bank_conflict_ways(_mfma16_b_read_addrs(False), 8, 32) == 2
     assert _bank_conflict_ways(_mfma16_b_read_addrs(True), 8, 32) == 1
+
+
+def _f32_epilogue_lds(swizzle=True):
+    """Byte addresses of the 16x16x32 instance's f32 C epilogue in one wave's
+    8 KiB LDS block (one 16-row block of the wave's 128x128 tile, 512-byte
+    rows): the ds_write_b128 of tile j by lane l (row l % 16, columns
+    16 j + 4 (l / 16) .. +3, chunk c = 4 j + l / 16 at c ^ row) and the
+    ds_read_b128 t by lane l (row 2 t + l / 32, chunk l % 32 at chunk ^ row)."""
+    sw = (lambda c, r: c ^ r) if swizzle else (lambda c, r: c)
+    writes = {j: [(l % 16) * 512 + sw(4 * j + l // 16, l % 16) * 16 for l in range(64)]
+              for j in range(8)}
+    reads = {t: [(2 * t + l // 32) * 512 + sw(l % 32, 2 * t + l // 32) * 16
+                 for l in range(64)] for t in range(8)}
+    return writes, reads
+
+
+def test_f32_epilogue_lds_map():
+    """The f32 C epilogue of the 16x16x32 instance: every element is written
+    to its own 16 bytes of the block, each whole-row read returns the row and
+    columns it stores, and both directions are free of bank conflicts at 16
+    lanes of 16 bytes per cycle. The chunk ^ row term is what makes them so:
+    without it a quarter wave's 16 rows share one bank group, 16-way."""
+    writes, reads = _f32_epilogue_lds()
+    held = {}
+    for j, addrs in writes.items():
+        for l, a in enumerate(addrs):
+            assert a % 16 == 0 and 0 <= a < 8192
+            held[a] = (l % 16, 16 * j + 4 * (l // 16))  # (row, first column)
+    assert len(held) == 8 * 64  # a bijection onto the 512 chunks of the block
+    for t, addrs in reads.items():
+        for l, a in enumerate(addrs):
+            assert held[a] == (2 * t + l // 32, 4 * (l % 32))
+    for addrs in list(writes.values()) + list(reads.values()):
+        assert _bank_conflict_ways(addrs, 16, 16) == 1
+    plain_w, plain_r = _f32_epilogue_lds(swizzle=False)
+    assert _bank_conflict_ways(plain_w[0], 16, 16) == 16
+    assert _bank_conflict_ways(plain_r[0], 16, 16) == 1  # reads are whole rows either way
