@@ -148,10 +148,11 @@ REFERENCE_CASES = (
 
 
 def _baseline_cases():
-    """The benchmark workloads of configs.py (f16 C = A*B), as FairCases."""
+    """The benchmark workloads of configs.py (f16 C = A*B, and the roofline
+    GEMM as f32 C += A*B), as FairCases."""
     from . import configs
     out = []
-    for w in configs.ALL:
+    for w in configs.ALL + configs.F32_ACCUMULATE:
         attrs = []
         if w.split_k > 1:
             attrs += [("tb.split-k", w.split_k), ("tb.reduction-mode", "split_k_serial")]
@@ -159,7 +160,8 @@ def _baseline_cases():
             attrs += [("tb.persistent", True), ("tb.num-ctas", w.num_ctas)]
         bm, bn, bk = w.block
         out.append(FairCase(w.name, w.M, w.N, w.K, bm, bn, bk, w.num_waves, w.stages,
-                            w.exact_tile, group_m=w.group_m, c_type="f16",
+                            w.exact_tile, group_m=w.group_m,
+                            c_type="f32" if w.c_f32 else "f16",
                             extra_module_attrs=tuple(attrs), seed=w.seed,
                             normal=w.dist == configs.NORMAL))
     return tuple(out)
