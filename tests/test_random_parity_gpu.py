@@ -43,6 +43,9 @@ def _case(rng, insts, case):
     if out == 0:
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, mapping=mapping,
                             split_k=1, reduction=tb.RED_NONE, num_programs=progs, **kw)
+    elif out == 1 and mfma16:  # plain f32 C (the 16x16x32 build has no split-K)
+        cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_ZERO, mapping=mapping,
+                            split_k=1, reduction=tb.RED_NONE, num_programs=progs, **kw)
     elif out == 1:
         s = rng.randint(2, 8)
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO,
@@ -109,7 +112,7 @@ def _fused_case(rng, insts, case):
     if out == 0:
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, mapping=mapping,
                             split_k=1, reduction=tb.RED_NONE, num_programs=progs, **kw)
-    elif out == 1 and rng.random() < 0.5:  # plain f32 store
+    elif out == 1 and (mfma16 or rng.random() < 0.5):  # plain f32 store (16x16x32: always)
         cfg = tb.GemmConfig(c_dtype=tb.DTYPE_F32, acc_init=tb.ACC_INIT_ZERO,
                             mapping=tb.MAP_TILE, split_k=1, reduction=tb.RED_NONE,
                             num_programs=tm * tn, **kw)
