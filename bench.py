@@ -32,6 +32,8 @@ sys.path.insert(0, ROOT)
 
 PEAK_TFLOPS_F16 = 2500.0  # MI355X dense FP16 MFMA (published, no sparsity)
 PEAK_HBM_GBS = 8000.0
+PEAK_CLOCK_MHZ = 2400.0  # the clock the dense peak is quoted at (1024 SIMDs x 1024 FLOP/clk)
+XCDS = 8  # MI355X: 8 XCDs of 32 CUs
 
 
 def log(msg: str) -> None:
@@ -89,18 +91,26 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
             torch.cuda.synchronize(device)
     for _ in range(warmup):
         launch()
-    walls, events = [], []
-    for _ in range(rounds):
+    walls, events, clocks = [], [], []
+    # shader-clock stamps (one wave per XCD) on the launch stream right before
+    # and after each round's timed region
+    stamps = torch.zeros((rounds, 2, 3 * XCDS), dtype=torch.int64, device=device)
+    for r in range(rounds):
         region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
+        tb.clock_stamp(stamps[r, 0], XCDS, stream=stream)
         region[0].record(stream)
         for _ in range(steps):
             launch()
         region[1].record(stream)
+        tb.clock_stamp(stamps[r, 1], XCDS, stream=stream)
         torch.cuda.synchronize(device)
         walls.append(time.perf_counter() - t0)
         events.append(region[0].elapsed_time(region[1]) / steps)
+    for r in range(rounds):
+        per_xcd = tb.shader_clock_mhz(stamps[r, 0].tolist(), stamps[r, 1].tolist())
+        clocks.append(statistics.mean(per_xcd.values()) if per_xcd else None)
     if C0 is not None:
         # the timed launches accumulated into C: check one more launch on the
         # prior C instead
@@ -109,7 +119,8 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
         torch.cuda.synchronize(device)
     ok = verify_output(w, A, B, C, bias, C0)
     return {"wall_s": statistics.median(walls), "avg_launch_ms": statistics.median(events),
-            "round_wall_s": walls, "round_launch_ms": events, "kernel": desc.kernel_name,
+            "round_wall_s": walls, "round_launch_ms": events, "round_clock_mhz": clocks,
+            "kernel": desc.kernel_name,
             "settle_launches": settle_launches, "verified": ok}
 
 
@@ -139,6 +150,21 @@ def verify_output(w, A, B, C, bias, C0=None):
     bad = int((~(err <= 1e-2 * (ref.abs() + 1))).sum().item())
     return {"rows": int(rows.numel()), "violations": bad,
             "max_abs_err": float(err.max().item()), "vs": "torch.matmul f32"}
+
+
+def clock_summary(r) -> dict:
+    """The effective shader clock of the timed rounds (stamps on the launch
+    stream around each round, mean over the 8 XCDs), the median round's value,
+    and the fraction of peak the kernel reaches per clock cycle: the achieved
+    rate scaled to the 2.4 GHz the peak is quoted at."""
+    clk = [c for c in r["round_clock_mhz"] if c]
+    if not clk:
+        return {"mhz": None}
+    mhz = statistics.median(clk)
+    return {"mhz": round(mhz, 1), "round_mhz": [round(c, 1) for c in clk],
+            "source": "s_memtime / s_memrealtime deltas of one wave per XCD on the "
+                      "launch stream before and after each timed round",
+            "peak_clock_mhz": PEAK_CLOCK_MHZ}
 
 
 def plan_time_ms(w, reps: int = 20) -> float:
@@ -261,9 +287,15 @@ def main() -> int:
     value = w.flop * args.steps / r["wall_s"] / 1e12
     avg_kernel_ms = r["avg_launch_ms"]
     achieved = w.flop / (avg_kernel_ms * 1e-3) / 1e12
+    clock = clock_summary(r)
+    if clock["mhz"]:
+        # per clock cycle: the fraction of the MFMA issue rate at the clock held
+        clock["frac_of_peak_at_clock"] = round(
+            achieved / (PEAK_TFLOPS_F16 * clock["mhz"] / PEAK_CLOCK_MHZ), 4)
     log(f"bench: {r['kernel']} wall {ms_per_step * 1e3:.1f} us/step, "
         f"kernel avg {avg_kernel_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s "
-        f"(rounds {[round(x * 1e3, 2) for x in r['round_launch_ms']]} us)")
+        f"(rounds {[round(x * 1e3, 2) for x in r['round_launch_ms']]} us, "
+        f"clock {clock})")
 
     extra = {}
     if not args.no_extra:
@@ -285,7 +317,8 @@ def main() -> int:
                 "frac_mfma_peak": round(other.flop / (us * 1e-6) / 1e12 / PEAK_TFLOPS_F16, 4),
                 "frac_hbm_peak": round(other.algo_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                 "plan_pipeline_ms": round(plan_time_ms(other), 3),
-                "kernel": o["kernel"], "verified_rows": o["verified"]["rows"]}
+                "kernel": o["kernel"], "verified_rows": o["verified"]["rows"],
+                "clock_mhz": clock_summary(o)["mhz"]}
             log(f"bench: {other.name}: {extra[other.name]}")
 
     cpu = None
@@ -321,6 +354,7 @@ def main() -> int:
                      "traffic_source": ("committed profile, not measured in this run: "
                                         f"profiles/traffic_{w.name}.json (rocprofv3 --pmc "
                                         "FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated)")},
+        "clock": clock,
         "timing": {"rounds": args.rounds, "statistic": "median over rounds",
                    "round_us_per_launch": [round(x * 1e3, 2) for x in r["round_launch_ms"]],
                    "round_ms_per_step_wall": [round(x * 1e3 / args.steps, 5)

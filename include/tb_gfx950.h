@@ -188,9 +188,10 @@ int tb_gemm_launch_ex(const tb_gemm_desc *desc, const void *a, const void *b,
  * more workspace than the scratch holds (tb_workspace_bytes). Every call on
  * one GPU shares that GPU's scratch: calls that overlap on one GPU (other
  * streams, other threads) race. Nothing in the scratch needs clearing: each
- * call writes every partial its reduction reads. No counterpart in the
- * reference, whose kernels keep their scratch in static shared memory
- * (LowerPipelineToNVGPU.cpp:2701-2712) and have no global workspace. */
+ * call writes every partial its reduction reads. The scratch belongs to the
+ * device of `stream` (the current device for the null stream). This entry
+ * point has no counterpart in the reference; it is for callers that cannot
+ * allocate. */
 int tb_gemm_launch_noalloc(const tb_gemm_desc *desc, const void *a, const void *b,
                            void *c, const void *bias, void *stream);
 
@@ -203,6 +204,17 @@ void tb_desc_free(tb_gemm_desc *desc);
  * Box-Muller normal (dist 1), times `scale`, rounded to nearest even. */
 int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
                        uint64_t seed, int32_t dist, double scale, void *stream);
+
+/* Harness helper (no reference counterpart; the reference's harness reads
+ * the GPU clock from nvidia-smi, tools/bench_stage1_fair.py:446-476). Launches
+ * `workgroups` one-wave workgroups on `stream`; workgroup w writes three
+ * uint64 to out[3w..3w+2]: the XCC (XCD) id it ran on, that XCD's shader
+ * clock counter (s_memtime) and the 100 MHz real-time counter
+ * (s_memrealtime). Workgroups are dealt to the XCDs round-robin, so 8 of
+ * them stamp every XCD of an MI355X. Two launches bracketing some work give
+ * each XCD's mean shader clock over it: shader-clock delta / real-time
+ * delta * 100 MHz, matched by XCC id. `out` is a device pointer. */
+int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream);
 
 /* Number of compiled kernel instances and the name of instance i. */
 int tb_kernel_count(void);

@@ -137,6 +137,8 @@ def lib() -> ctypes.CDLL:
     L.tb_fill_seeded_f16.argtypes = [vp, i64, i64, i64, ctypes.c_uint64, i32,
                                      ctypes.c_double, vp]
     L.tb_fill_seeded_f16.restype = ctypes.c_int
+    L.tb_clock_stamp.argtypes = [vp, i32, vp]
+    L.tb_clock_stamp.restype = ctypes.c_int
     L.tb_kernel_count.restype = ctypes.c_int
     L.tb_kernel_name.argtypes = [ctypes.c_int]
     L.tb_kernel_name.restype = ctypes.c_char_p
@@ -357,6 +359,30 @@ def fill_seeded_f16(dst, rows: int, cols: int, seed: int, dist: int = 0,
     _check(lib().tb_fill_seeded_f16(_ptr(dst), rows, cols,
                                     cols if ld is None else ld, seed, dist,
                                     scale, _stream_handle(stream)))
+
+
+def clock_stamp(out, workgroups: int = 8, stream=None) -> None:
+    """Stamp (XCC id, shader clock, 100 MHz clock) from `workgroups` one-wave
+    workgroups into the uint64 device tensor `out` (3 per workgroup), on
+    `stream`. Workgroups go to the XCDs round-robin: 8 stamp every XCD."""
+    _check(lib().tb_clock_stamp(_ptr(out), workgroups, _stream_handle(stream)))
+
+
+def shader_clock_mhz(before, after) -> dict:
+    """Mean shader clock per XCD between two clock_stamp readings (host
+    lists of uint64 triples), matched by XCC id: delta(shader clock) /
+    delta(100 MHz clock) * 100 MHz. Returns {xcc: MHz}."""
+    b = {int(before[3 * i]): (int(before[3 * i + 1]), int(before[3 * i + 2]))
+         for i in range(len(before) // 3)}
+    out = {}
+    for i in range(len(after) // 3):
+        x = int(after[3 * i])
+        if x in b:
+            dt = int(after[3 * i + 1]) - b[x][0]
+            drt = int(after[3 * i + 2]) - b[x][1]
+            if drt > 0:
+                out[x] = dt / drt * 100.0
+    return out
 
 
 def kernel_names() -> list[str]:

@@ -136,6 +136,32 @@ __global__ __launch_bounds__(256) void fill_kernel(uint16_t *dst, int64_t rows,
   }
 }
 
+// ---- clock stamps --------------------------------------------------------
+// Workgroup b (one wave) writes out[3b] = the XCC (XCD) it ran on,
+// out[3b+1] = the shader-clock counter (s_memtime) and out[3b+2] = the
+// constant 100 MHz counter (s_memrealtime). Workgroups are dealt to the XCDs
+// round-robin, so `xcds` workgroups stamp every XCD once. Each XCD keeps
+// its own shader-clock counter: two stamps are compared per XCC id, and the
+// shader-clock delta over the real-time delta is that XCD's mean clock
+// between them. Only lane 0 stores (vector stores).
+__global__ __launch_bounds__(64) void clock_stamp_kernel(unsigned long long *out) {
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
+  unsigned long long t, rt;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(rt)::"memory");
+  if (threadIdx.x == 0) {
+    out[3 * blockIdx.x + 0] = xcc & 0xfu;
+    out[3 * blockIdx.x + 1] = t;
+    out[3 * blockIdx.x + 2] = rt;
+  }
+}
+
+hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s) {
+  hipLaunchKernelGGL(clock_stamp_kernel, dim3(workgroups), dim3(64), 0, s, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_reduce_ex(const float *ws, void *C, int M, int N, int ldc,
                             int split_k, int c_f16, int load_c, const EpiArgs &epi,
                             hipStream_t s) {

@@ -222,5 +222,7 @@ hipError_t launch_reduce_ex(const float *ws, void *C, int M, int N, int ldc,
                             hipStream_t s);
 hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
                        uint64_t seed, int dist, double scale, hipStream_t s);
+// `workgroups` one-wave stamps of (XCC id, shader clock, 100 MHz clock).
+hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s);
 
 } // namespace tbk

@@ -890,9 +890,11 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         const int i = l - LA;
         const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
         const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
+        // unsigned: a lookahead k-tile past the end (voffset kOob) may put
+        // k0 past K, where the signed product could pass INT_MAX
         load_lds16(rb4, b_lds + i * NW * 1024u,
                    (kt_ok && krow < p.K) ? b_voff : kOob,
-                   (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
+                   (uint32_t)(k0 + i * T::B_ROWS_PER_LOAD) * (uint32_t)p.ldb * 2u);
       }
     };
     auto issue_tile = [&](int kt, int stage) {
@@ -1446,7 +1448,7 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
           const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
           const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
           load_lds16(rb4, b_lds + i * NW * 1024u, (kt_ok && krow < p.K) ? b_voff : kOob,
-                     (k0 + i * T::B_ROWS_PER_LOAD) * p.ldb * 2);
+                     (uint32_t)(k0 + i * T::B_ROWS_PER_LOAD) * (uint32_t)p.ldb * 2u);
         }
       };
       auto issue_tile = [&](int kt, int stage) {

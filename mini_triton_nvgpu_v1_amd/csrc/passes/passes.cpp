@@ -451,7 +451,9 @@ void lowerToGfx950(Module &m, const PassOptions &) {
     const InstanceSchedule sched = instanceSchedule(instanceKeyOf(g));
     launch.attrs["waits"] = Dense({sched.vmPrologue, sched.vmLoop, sched.lgkmLoop});
     launch.attrs["grid"] = Dense({g.num_programs, 1, 1});
-    launch.attrs["block"] = Dense({g.num_waves * k.target.threadsPerWarp, 1, 1});
+    // the wave grid's waves plus the instance's load-only waves, if any
+    launch.attrs["block"] =
+        Dense({(g.num_waves + sched.loaderWaves) * k.target.threadsPerWarp, 1, 1});
     launch.attrs["lds_bytes"] = I64(k.sharedWorkspace.totalBytes);
     launch.attrs["workspace_bytes"] = I64(k.resourceClosure.globalWorkspaceBytes);
     op = launch;

@@ -214,18 +214,37 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_address(void **out) {
+// The scratch of the device the kernels run on: the stream's device (the
+// current device for the null stream). Its address is looked up once, with
+// that device made current for the lookup and the caller's current device
+// restored afterwards.
+int scratch_address(hipStream_t stream, void **out) {
   int dev = 0;
-  if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice"))
+  if (stream) {
+    hipDevice_t sd = 0;
+    if (int rc = check_hip(hipStreamGetDevice(stream, &sd), "hipStreamGetDevice"))
+      return rc;
+    dev = (int)sd;
+  } else if (int rc = check_hip(hipGetDevice(&dev), "hipGetDevice")) {
     return rc;
+  }
   if (dev < 0 || dev >= kMaxDevices)
     return fail("tb_gemm_launch_noalloc: device index " + std::to_string(dev) +
                 " beyond the library's table of " + std::to_string(kMaxDevices));
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    if (int rc = check_hip(hipGetDevice(&cur), "hipGetDevice"))
+      return rc;
+    if (cur != dev)
+      if (int rc = check_hip(hipSetDevice(dev), "hipSetDevice"))
+        return rc;
     void *ptr = nullptr;
-    if (int rc = check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)),
-                           "hipGetSymbolAddress(scratch)"))
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev)
+      if (int rc = check_hip(hipSetDevice(cur), "hipSetDevice (restore)"))
+        return rc;
+    if (int rc = check_hip(e, "hipGetSymbolAddress(scratch)"))
       return rc;
     if (!ptr)
       return fail("tb_gemm_launch_noalloc: hipGetSymbolAddress returned no address");
@@ -376,7 +395,7 @@ int tb_gemm_launch_noalloc(const tb_gemm_desc *d, const void *a, const void *b,
                   " bytes of split-K workspace, more than the library's static scratch of " +
                   std::to_string((size_t)TB_NOALLOC_SCRATCH_BYTES) +
                   " bytes; use tb_gemm_launch_ex with a caller-provided workspace");
-    if (int rc = scratch_address(&ws))
+    if (int rc = scratch_address(reinterpret_cast<hipStream_t>(stream), &ws))
       return rc;
   }
   return launch_impl(d, a, b, c, bias, ws, stream, "tb_gemm_launch_noalloc");
@@ -391,6 +410,16 @@ int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
   return check_hip(tbk::launch_fill(dst, rows, cols, ld, seed, dist, scale,
                                     reinterpret_cast<hipStream_t>(stream)),
                    "hipLaunchKernel(fill)");
+}
+
+int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream) {
+  if (!out || workgroups < 1 || workgroups > 1024)
+    return fail("tb_clock_stamp: out must be a device pointer and workgroups in 1..1024");
+  if (reinterpret_cast<uintptr_t>(out) % 8)
+    return fail("tb_clock_stamp: out must be 8-byte aligned");
+  return check_hip(tbk::launch_clock_stamp(reinterpret_cast<unsigned long long *>(out),
+                                           workgroups, reinterpret_cast<hipStream_t>(stream)),
+                   "hipLaunchKernel(clock stamp)");
 }
 
 int tb_kernel_count(void) { return tbk::kernel_count(); }

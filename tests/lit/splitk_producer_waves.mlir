@@ -7,8 +7,9 @@
 // issue the direct-to-LDS loads (3 per lane per k-tile). They issue k-tiles
 // 0..2 in the prologue and wait for k-tile 0 only (vmcnt(6)); at each
 // barrier the next k-tile has landed (vmcnt(3)) and the stage the barrier
-// frees is refilled whole. The f16 instance of the same tile keeps the
-// general loop, whose waits are the same ("burst") without loader waves.
+// frees is refilled whole. The launch's block counts both halves: 16 waves
+// of 64 lanes. The f16 instance of the same tile keeps the general loop,
+// whose waits are the same ("burst") without loader waves.
 module attributes {"tb.num-warps" = 8 : i64, "tb.requested-stages" = 3 : i64,
                    "tb.split-k" = 8 : i64,
                    "tb.reduction-mode" = "split_k_serial"} {
@@ -22,6 +23,7 @@ module attributes {"tb.num-warps" = 8 : i64, "tb.requested-stages" = 3 : i64,
 }
 
 // CHECK: tb.gfx950_launch
+// CHECK-SAME: block = array<i64: 1024, 1, 1>
 // CHECK-SAME: mapping = 2 : i64
 // CHECK-SAME: reduction = 1 : i64
 // CHECK-SAME: split_k = 8 : i64

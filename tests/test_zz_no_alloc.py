@@ -100,3 +100,32 @@ def test_noalloc_matches_the_workspace_entry_point(device):
         print(f"  {desc.kernel_name}: bit-identical, violations={bad} max|err|={err:.3e}",
               flush=True)
         assert bad == 0, f"{w.name}: {bad} elements outside tolerance, worst {err} at {worst}"
+
+
+@pytest.mark.gpu
+def test_noalloc_allocates_no_device_memory(device):
+    """The defining property: after one warm-up call (which loads the code
+    object holding the scratch), further split-K calls leave the device's free
+    memory unchanged. Every buffer the calls use is allocated before the
+    first reading of hipMemGetInfo, and nothing else allocates in between."""
+    import torch
+    stream = torch.cuda.current_stream(device)
+    w = _case("splitk_512x512x16384", 512, 512, 16384, 8, 0x5EED0005)
+    small = _case("splitk_ragged_200x120x2000", 200, 120, 2000, 3, 0x5EED0D01)
+    descs = [tb.plan_from_mlir(x.mlir()) for x in (w, small)]
+    bufs = []
+    for x in (w, small):
+        A, B = oracle.config_inputs(x.M, x.N, x.K, x.seed, x.dist)
+        bufs.append((torch.from_numpy(A).to(device), torch.from_numpy(B).to(device),
+                     torch.empty((x.M, x.N), dtype=torch.float16, device=device)))
+    for d, (a, b, c) in zip(descs, bufs):  # warm-up: code objects and scratch loaded
+        _noalloc(d, a, b, c, stream=stream)
+    torch.cuda.synchronize(device)
+    free0, total = torch.cuda.mem_get_info(device)
+    for _ in range(5):
+        for d, (a, b, c) in zip(descs, bufs):
+            _noalloc(d, a, b, c, stream=stream)
+    torch.cuda.synchronize(device)
+    free1, _ = torch.cuda.mem_get_info(device)
+    print(f"free device memory before {free0} after {free1} of {total}", flush=True)
+    assert free1 == free0, f"free device memory changed by {free0 - free1} bytes"
