@@ -34,6 +34,7 @@ PEAK_TFLOPS_F16 = 2500.0  # MI355X dense FP16 MFMA (published, no sparsity)
 PEAK_HBM_GBS = 8000.0
 PEAK_CLOCK_MHZ = 2400.0  # the clock the dense peak is quoted at (1024 SIMDs x 1024 FLOP/clk)
 XCDS = 8  # MI355X: 8 XCDs of 32 CUs
+PROBE_TICKS = 2000  # clock-probe window: 20 us of the 100 MHz counter
 
 
 def log(msg: str) -> None:
@@ -92,25 +93,22 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
     for _ in range(warmup):
         launch()
     walls, events, clocks = [], [], []
-    # shader-clock stamps (one wave per XCD) on the launch stream right before
-    # and after each round's timed region
-    stamps = torch.zeros((rounds, 2, 3 * XCDS), dtype=torch.int64, device=device)
+    # a shader-clock probe (one wave per XCD, 20 us) on the launch stream right
+    # after each round's timed region: the clock the round's kernels ran at
+    probes = torch.zeros((rounds, 3 * XCDS), dtype=torch.int64, device=device)
     for r in range(rounds):
         region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
-        tb.clock_stamp(stamps[r, 0], XCDS, stream=stream)
         region[0].record(stream)
         for _ in range(steps):
             launch()
         region[1].record(stream)
-        tb.clock_stamp(stamps[r, 1], XCDS, stream=stream)
+        tb.clock_probe(probes[r], XCDS, PROBE_TICKS, stream=stream)
         torch.cuda.synchronize(device)
         walls.append(time.perf_counter() - t0)
         events.append(region[0].elapsed_time(region[1]) / steps)
-    for r in range(rounds):
-        per_xcd = tb.shader_clock_mhz(stamps[r, 0].tolist(), stamps[r, 1].tolist())
-        clocks.append(statistics.mean(per_xcd.values()) if per_xcd else None)
+    clocks = [tb.probe_clock_mhz(p) for p in probes.tolist()]
     if C0 is not None:
         # the timed launches accumulated into C: check one more launch on the
         # prior C instead
@@ -153,17 +151,17 @@ def verify_output(w, A, B, C, bias, C0=None):
 
 
 def clock_summary(r) -> dict:
-    """The effective shader clock of the timed rounds (stamps on the launch
-    stream around each round, mean over the 8 XCDs), the median round's value,
-    and the fraction of peak the kernel reaches per clock cycle: the achieved
-    rate scaled to the 2.4 GHz the peak is quoted at."""
+    """The shader clock of the timed rounds (a probe on the launch stream
+    right after each round, mean over the 8 XCDs), the median round's value.
+    The caller adds the fraction of peak the kernel reaches per clock cycle:
+    the achieved rate over the peak scaled from 2.4 GHz to that clock."""
     clk = [c for c in r["round_clock_mhz"] if c]
     if not clk:
         return {"mhz": None}
     mhz = statistics.median(clk)
     return {"mhz": round(mhz, 1), "round_mhz": [round(c, 1) for c in clk],
-            "source": "s_memtime / s_memrealtime deltas of one wave per XCD on the "
-                      "launch stream before and after each timed round",
+            "source": "s_memtime / s_memrealtime over a 20 us window, one wave per XCD, "
+                      "launched on the stream right after each timed round",
             "peak_clock_mhz": PEAK_CLOCK_MHZ}
 
 

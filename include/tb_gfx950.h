@@ -207,14 +207,15 @@ int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
 
 /* Harness helper (no reference counterpart; the reference's harness reads
  * the GPU clock from nvidia-smi, tools/bench_stage1_fair.py:446-476). Launches
- * `workgroups` one-wave workgroups on `stream`; workgroup w writes three
- * uint64 to out[3w..3w+2]: the XCC (XCD) id it ran on, that XCD's shader
- * clock counter (s_memtime) and the 100 MHz real-time counter
- * (s_memrealtime). Workgroups are dealt to the XCDs round-robin, so 8 of
- * them stamp every XCD of an MI355X. Two launches bracketing some work give
- * each XCD's mean shader clock over it: shader-clock delta / real-time
- * delta * 100 MHz, matched by XCC id. `out` is a device pointer. */
-int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream);
+ * `workgroups` one-wave workgroups on `stream`; each measures the shader
+ * clock of its CU over `window_ticks` ticks of the 100 MHz real-time counter
+ * (s_memtime and s_memrealtime read by the same wave at both ends) and
+ * writes three uint64 to out[3w..3w+2]: its XCC (XCD) id, the shader-clock
+ * cycles and the 100 MHz ticks of the window (clock = cycles / ticks * 100
+ * MHz). Workgroups are dealt to the XCDs round-robin, so 8 of them cover
+ * every XCD of an MI355X. Launched right after some work on the same stream,
+ * it reads the clock that work ran at. `out` is a device pointer. */
+int tb_clock_probe(uint64_t *out, int32_t workgroups, int32_t window_ticks, void *stream);
 
 /* Number of compiled kernel instances and the name of instance i. */
 int tb_kernel_count(void);

@@ -137,8 +137,8 @@ def lib() -> ctypes.CDLL:
     L.tb_fill_seeded_f16.argtypes = [vp, i64, i64, i64, ctypes.c_uint64, i32,
                                      ctypes.c_double, vp]
     L.tb_fill_seeded_f16.restype = ctypes.c_int
-    L.tb_clock_stamp.argtypes = [vp, i32, vp]
-    L.tb_clock_stamp.restype = ctypes.c_int
+    L.tb_clock_probe.argtypes = [vp, i32, i32, vp]
+    L.tb_clock_probe.restype = ctypes.c_int
     L.tb_kernel_count.restype = ctypes.c_int
     L.tb_kernel_name.argtypes = [ctypes.c_int]
     L.tb_kernel_name.restype = ctypes.c_char_p
@@ -361,28 +361,19 @@ def fill_seeded_f16(dst, rows: int, cols: int, seed: int, dist: int = 0,
                                     scale, _stream_handle(stream)))
 
 
-def clock_stamp(out, workgroups: int = 8, stream=None) -> None:
-    """Stamp (XCC id, shader clock, 100 MHz clock) from `workgroups` one-wave
-    workgroups into the uint64 device tensor `out` (3 per workgroup), on
-    `stream`. Workgroups go to the XCDs round-robin: 8 stamp every XCD."""
-    _check(lib().tb_clock_stamp(_ptr(out), workgroups, _stream_handle(stream)))
+def clock_probe(out, workgroups: int = 8, window_ticks: int = 2000, stream=None) -> None:
+    """Probe the shader clock from `workgroups` one-wave workgroups over
+    `window_ticks` ticks of the 100 MHz counter, into the 64-bit device tensor
+    `out` (XCC id, cycles, ticks per workgroup), on `stream`."""
+    _check(lib().tb_clock_probe(_ptr(out), workgroups, window_ticks, _stream_handle(stream)))
 
 
-def shader_clock_mhz(before, after) -> dict:
-    """Mean shader clock per XCD between two clock_stamp readings (host
-    lists of uint64 triples), matched by XCC id: delta(shader clock) /
-    delta(100 MHz clock) * 100 MHz. Returns {xcc: MHz}."""
-    b = {int(before[3 * i]): (int(before[3 * i + 1]), int(before[3 * i + 2]))
-         for i in range(len(before) // 3)}
-    out = {}
-    for i in range(len(after) // 3):
-        x = int(after[3 * i])
-        if x in b:
-            dt = int(after[3 * i + 1]) - b[x][0]
-            drt = int(after[3 * i + 2]) - b[x][1]
-            if drt > 0:
-                out[x] = dt / drt * 100.0
-    return out
+def probe_clock_mhz(readings) -> float | None:
+    """The mean shader clock of a clock_probe reading (a host list of
+    (XCC id, cycles, ticks) triples): total cycles / total ticks * 100 MHz."""
+    cyc = sum(int(readings[3 * i + 1]) for i in range(len(readings) // 3))
+    ticks = sum(int(readings[3 * i + 2]) for i in range(len(readings) // 3))
+    return cyc / ticks * 100.0 if ticks > 0 else None
 
 
 def kernel_names() -> list[str]:

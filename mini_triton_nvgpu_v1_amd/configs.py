@@ -51,6 +51,29 @@ def wave_grid(block_m: int, block_n: int, num_waves: int, instr: int = 32):
     return best
 
 
+_M16_TILES = None
+
+
+def mfma16_tiles() -> set:
+    """(BM, BN, BK, wave grid M, wave grid N, stages) of every 16x16x32
+    instance: the hand-scheduled tile and the TBK_M16_TILES_* lists of
+    csrc/kernels/gemm_tiles.h, read from the header the kernels and the
+    plan's instance table are built from."""
+    global _M16_TILES
+    if _M16_TILES is None:
+        import os
+        import re
+        path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "csrc", "kernels",
+                            "gemm_tiles.h")
+        text = open(path).read()
+        tiles = {(256, 256, 64, 2, 2, 2)}
+        for m in re.finditer(r"#define TBK_M16_TILES_\w+\(X\)((?:.*\\\n)*.*)", text):
+            for t in re.findall(r"X\(([^)]*)\)", m.group(1)):
+                tiles.add(tuple(int(v) for v in t.split(",")))
+        _M16_TILES = tiles
+    return _M16_TILES
+
+
 @dataclass(frozen=True)
 class Workload:
     name: str
@@ -175,10 +198,14 @@ class Workload:
             mfma=MFMA_16X16X32 if self.mfma16_supported() else MFMA_32X32X16)
 
     def mfma16_supported(self) -> bool:
-        """The plan's choice of v_mfma_f32_16x16x32_f16: the 4-wave
-        256x256x64 2-stage tile (f16 or f32 C), any M, N and K, no split-K."""
-        return (self.block == (256, 256, 64) and self.num_waves == 4 and self.stages == 2
-                and self.split_k == 1)
+        """The plan's choice of v_mfma_f32_16x16x32_f16 (without an `mma`
+        attribute): every tile with a 16x16x32 instance on the plan's wave
+        grid (the hand-scheduled 4-wave 256x256x64 2-stage tile and the
+        16x16x32 loop's lists), f16 or f32 C, any M, N and K, no split-K."""
+        if self.split_k != 1:
+            return False
+        wg = wave_grid(*self.block[:2], self.num_waves)
+        return (*self.block, *wg, self.stages) in mfma16_tiles()
 
 
 SMOKE = Workload("smoke_64x64x32", 64, 64, 32, 0x5EED0001, UNIFORM,

@@ -136,29 +136,47 @@ __global__ __launch_bounds__(256) void fill_kernel(uint16_t *dst, int64_t rows,
   }
 }
 
-// ---- clock stamps --------------------------------------------------------
-// Workgroup b (one wave) writes out[3b] = the XCC (XCD) it ran on,
-// out[3b+1] = the shader-clock counter (s_memtime) and out[3b+2] = the
-// constant 100 MHz counter (s_memrealtime). Workgroups are dealt to the XCDs
-// round-robin, so `xcds` workgroups stamp every XCD once. Each XCD keeps
-// its own shader-clock counter: two stamps are compared per XCC id, and the
-// shader-clock delta over the real-time delta is that XCD's mean clock
-// between them. Only lane 0 stores (vector stores).
-__global__ __launch_bounds__(64) void clock_stamp_kernel(unsigned long long *out) {
+// ---- clock probe ---------------------------------------------------------
+// Workgroup b (one wave) measures the shader clock of the CU it runs on:
+// it reads the shader-clock counter (s_memtime) and the constant 100 MHz
+// counter (s_memrealtime), spins until `window` ticks of the latter have
+// passed (at most 2^20 reads: every wave exits), and reads both again. Both
+// readings of a pair come from the same wave, so the counters' per-CU
+// offsets cancel. out[3b] = the XCC (XCD) id, out[3b+1] = shader-clock
+// cycles, out[3b+2] = 100 MHz ticks of the window; cycles / ticks * 100 MHz
+// is the clock. Launched right after a stretch of work, it reads the clock
+// that work ran at (the power manager reacts on a millisecond scale). Only
+// lane 0 stores (vector stores).
+__device__ __forceinline__ unsigned long long read_shader_clock() {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+  return t;
+}
+__device__ __forceinline__ unsigned long long read_real_clock() {
+  unsigned long long t;
+  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+  return t;
+}
+
+__global__ __launch_bounds__(64) void clock_probe_kernel(unsigned long long *out,
+                                                         unsigned window) {
   unsigned xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
-  unsigned long long t, rt;
-  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
-  asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(rt)::"memory");
+  const unsigned long long t0 = read_shader_clock(), r0 = read_real_clock();
+  for (int i = 0; i < (1 << 20); ++i)
+    if (read_real_clock() - r0 >= window)
+      break;
+  const unsigned long long t1 = read_shader_clock(), r1 = read_real_clock();
   if (threadIdx.x == 0) {
     out[3 * blockIdx.x + 0] = xcc & 0xfu;
-    out[3 * blockIdx.x + 1] = t;
-    out[3 * blockIdx.x + 2] = rt;
+    out[3 * blockIdx.x + 1] = t1 - t0;
+    out[3 * blockIdx.x + 2] = r1 - r0;
   }
 }
 
-hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s) {
-  hipLaunchKernelGGL(clock_stamp_kernel, dim3(workgroups), dim3(64), 0, s, out);
+hipError_t launch_clock_probe(unsigned long long *out, int workgroups, unsigned window,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(clock_probe_kernel, dim3(workgroups), dim3(64), 0, s, out, window);
   return hipGetLastError();
 }
 
@@ -187,13 +205,19 @@ hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
 }
 
 // ---- instance registry ----------------------------------------------------
-// One table per shape and flavour (gemm_inst.hip) plus the 16x16x32 tables
-// (f16 C; f32 C).
+// One table per shape and flavour (gemm_inst.hip), the hand-scheduled
+// 16x16x32 tables (f16 C; f32 C) and one 16x16x32 table per shape and
+// flavour of TBK_M16_SHAPES (gemm_inst_mfma16g.hip).
 #define TBK_DECLARE(SHAPE)                                                      \
   const KernelEntry *entries_##SHAPE(int *n);                                  \
   const KernelEntry *entries_##SHAPE##_epi(int *n);
 TBK_SHAPES(TBK_DECLARE)
 #undef TBK_DECLARE
+#define TBK_DECLARE_M16(SHAPE)                                                  \
+  const KernelEntry *entries_m16_##SHAPE(int *n);                              \
+  const KernelEntry *entries_m16_##SHAPE##_epi(int *n);
+TBK_M16_SHAPES(TBK_DECLARE_M16)
+#undef TBK_DECLARE_M16
 const KernelEntry *entries_mfma16(int *n);
 const KernelEntry *entries_mfma16_f32(int *n);
 const KernelEntry *entries_producer(int *n);
@@ -216,9 +240,12 @@ static const KernelEntry *preferred(const KernelEntry *e) {
 }
 
 #define TBK_TABLES(SHAPE) entries_##SHAPE, entries_##SHAPE##_epi,
+#define TBK_M16_TABLES(SHAPE) entries_m16_##SHAPE, entries_m16_##SHAPE##_epi,
 static const KernelEntry *(*const kTables[])(int *) = {
-    TBK_SHAPES(TBK_TABLES) entries_mfma16, entries_mfma16_f32};
+    TBK_SHAPES(TBK_TABLES) entries_mfma16, entries_mfma16_f32,
+    TBK_M16_SHAPES(TBK_M16_TABLES)};
 #undef TBK_TABLES
+#undef TBK_M16_TABLES
 
 int kernel_count() {
   int total = 0;

@@ -108,17 +108,25 @@ __device__ __forceinline__ float epi_activation(float x, int act) {
 typedef float epi_f32x4 __attribute__((ext_vector_type(4)));
 
 // Bias values of columns col .. col+3 (zero past N: those columns are never
-// stored). N % 4 == 0, so a group is wholly inside or outside.
+// stored). N % 4 == 0, so a group is wholly inside or outside. A buffer load
+// whose records end at column N: columns past N read zeros without a
+// per-lane branch (only the bias kind, a kernel argument, branches), so no
+// divergent control flow lands in an epilogue that holds the accumulators.
 __device__ __forceinline__ epi_f32x4 epi_load_bias(const EpiArgs &e, int col, int N) {
   epi_f32x4 b = {0.f, 0.f, 0.f, 0.f};
-  if (e.bias_kind == 0 || col >= N)
+  if (e.bias_kind == 0)
     return b;
+  const uint32_t off = col < N ? (uint32_t)col : 0x40000000u; // past N: out of range
   if (e.bias_kind == 1) {
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    const h4 h = *reinterpret_cast<const h4 *>(static_cast<const _Float16 *>(e.bias) + col);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(e.bias), 0, N * 2, 0x00020000);
+    const h4 h = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(r, off * 2u, 0, 0));
     b = (epi_f32x4){(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
   } else {
-    b = *reinterpret_cast<const epi_f32x4 *>(static_cast<const float *>(e.bias) + col);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(e.bias), 0, N * 4, 0x00020000);
+    b = __builtin_bit_cast(epi_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off * 4u, 0, 0));
   }
   return b;
 }
@@ -222,7 +230,9 @@ hipError_t launch_reduce_ex(const float *ws, void *C, int M, int N, int ldc,
                             hipStream_t s);
 hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
                        uint64_t seed, int dist, double scale, hipStream_t s);
-// `workgroups` one-wave stamps of (XCC id, shader clock, 100 MHz clock).
-hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s);
+// `workgroups` one-wave probes of (XCC id, shader-clock cycles, 100 MHz
+// ticks) over a window of `window` ticks.
+hipError_t launch_clock_probe(unsigned long long *out, int workgroups, unsigned window,
+                              hipStream_t s);
 
 } // namespace tbk

@@ -73,6 +73,52 @@ __device__ __forceinline__ void load_lds16_at(u32x4 rsrc, uint32_t lds_base, uin
                : "memory", "scc");
 }
 
+// The lane index computed afresh (mbcnt) behind an empty asm, for code
+// after a main loop: the compiler can neither reuse a lane-derived value
+// that the loop would have to keep live nor hoist the epilogue's addresses
+// (derived from it) into the loop, where they would hold registers the loop
+// needs.
+__device__ __forceinline__ int lane_id_fresh() {
+  int l = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  asm volatile("" : "+v"(l));
+  return l;
+}
+
+// The kernel's GemmParams argument read again from the kernel-argument
+// segment (its only argument, at offset 0) through an opaque pointer, for
+// code after a main loop: the fields it uses are then loaded there (scalar
+// loads) instead of being held in scalar registers across the loop (the
+// fused epilogue's arguments would otherwise push the loop's scalar
+// registers into spills).
+typedef const __attribute__((address_space(4))) GemmParams *kernarg_params_ptr;
+__device__ __forceinline__ GemmParams params_fresh() {
+  kernarg_params_ptr q = (kernarg_params_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(q));
+  GemmParams r;
+  r.A = q->A, r.B = q->B, r.C = q->C, r.ws = q->ws;
+  r.M = q->M, r.N = q->N, r.K = q->K, r.lda = q->lda, r.ldb = q->ldb, r.ldc = q->ldc;
+  r.tiles_m = q->tiles_m, r.tiles_n = q->tiles_n, r.tiles_k = q->tiles_k;
+  r.group_m = q->group_m, r.split_k = q->split_k, r.mapping = q->mapping;
+  r.total_work = q->total_work, r.xcds = q->xcds, r.ws_ld = q->ws_ld;
+  r.bias = q->bias, r.epi_bias = q->epi_bias, r.epi_act = q->epi_act;
+  r.epi_clamp = q->epi_clamp, r.clamp_lo = q->clamp_lo, r.clamp_hi = q->clamp_hi;
+  return r;
+}
+
+// First statement of each variant of a dispatched epilogue: an empty asm
+// that differs per (activation, clamp), so the variants no longer begin with
+// the same code, and a scheduling barrier that keeps the variant's own code
+// below it. Otherwise the compiler hoists their common start (the
+// accumulator reads of every element) above the dispatch, holding the whole
+// tile in VGPRs at once (the fused 16x16x32 build spilled).
+template <int ACT, bool CLAMP>
+__device__ __forceinline__ void epi_variant_fence() {
+  asm volatile("; fused epilogue variant %0 %1" ::"i"(ACT), "i"(CLAMP ? 1 : 0));
+  __builtin_amdgcn_sched_barrier(0); // nothing scheduled above it
+}
+
+
+
 // f(std::integral_constant<int, i>{}) for i = 0 .. N-1, in order.
 template <class F, int... I>
 __device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int, I...>) {
@@ -81,6 +127,21 @@ __device__ __forceinline__ void static_for_seq(F &&f, std::integer_sequence<int,
 template <int N, class F>
 __device__ __forceinline__ void static_for(F &&f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// Runs block(i, act, clamp) for the epilogue's 16-row blocks i = 0 .. NB-1,
+// with EPI the activation and clamp of the launch dispatched once per block
+// (a block's code is specialised to them); without, the plain block.
+// Dispatched per block rather than once for the whole tile, a variant reads
+// only one block's accumulators, whatever the compiler hoists above it.
+template <int NB, bool EPI, class F>
+__device__ __forceinline__ void epi_for_blocks(const GemmParams &pe, F &&block) {
+  static_for<NB>([&](auto i_c) {
+    if constexpr (EPI)
+      epi_dispatch(pe.epi_act, pe.epi_clamp, [&](auto a, auto c) { block(i_c, a, c); });
+    else
+      block(i_c, std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+  });
 }
 
 // Raw buffer descriptor as four dwords for inline asm operands ("s"): the
@@ -337,7 +398,10 @@ constexpr int kMfma16LgkmLoop = 0;
 
 // OUT: kOutF16 (f16 C), kOutF32Partial (a plain f32 C store: never split-K
 // here) or kOutF32Accum (f32 C += A*B); the main loop is the same for all.
-template <int OUT, bool EPI, bool KPART>
+// Whole k-tiles only: a problem with K % 64 != 0 runs the 16x16x32 loop's
+// build of this tile (gemm_mfma16g, the entry's partial-K kernel), which
+// masks the partial last k-tile, so this build carries no masking code.
+template <int OUT, bool EPI>
 __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0, u32x4 *lds) {
   static_assert(OUT == kOutF16 || OUT == kOutF32Partial || OUT == kOutF32Accum,
                 "no atomic or split-K output on the 16x16x32 instance");
@@ -351,11 +415,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(TBK_LDS void *)lds;
-  // KPART: the build for K % 64 != 0 (the last k-tile is partial); the
-  // launcher takes it only then, so the whole-K build carries none of its
-  // masking code
-  const int nk = (p.K + BK - 1) / BK; // k-tiles
-  const int kfull = p.K / BK;          // whole k-tiles
+  const int nk = p.K / BK; // k-tiles (K % 64 == 0 here)
 
   // Direct loads: round l of wave w fills 1 KiB at slot + l * 4 KiB + w * 1 KiB
   // (A rows 32l + 8w .. +7; B k-rows 8l + 2w, +1). B's 16-byte chunk c of
@@ -366,15 +426,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // chunk in every A round and one per round parity in B; only the scalar
   // offset moves.
   // Ragged edges. A round l covers rows m0 + a_row0 + 32l and is loaded only
-  // while that row is below M; B columns at or past N load from kOob. In a
-  // partial last k-tile (K % 64 = 8r, r = 1..7) a lane's A chunk holds
-  // k = 64 kfull + 8 a_lc and loads from kOob unless a_lc < r, and B round l
-  // holds k rows 64 kfull + 8l .. +7, so rounds l >= r take a descriptor of
-  // zero records. Every such element is refused here, by its offset or its
-  // descriptor, rather than left to the buffer range check (the window's
-  // records reach the matrix end, not the edge of the problem). Past the edges the
-  // ring holds zeros: in M and N they only reach C elements that are not
-  // stored, in K they add nothing.
+  // while that row is below M; B columns at or past N load from kOob. Every
+  // such element is refused here, by its offset, rather than left to the
+  // buffer range check. Past the edges the ring holds zeros, which only
+  // reach C elements that are not stored.
   const int a_row0 = (wave * 64 + lane) >> 3;
   const int a_lc = (lane & 7) ^ ((a_row0 >> 1) & 7);
   const int a_rows_left = p.M - m0 - a_row0;
@@ -396,33 +451,22 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   const uint32_t a_bytes = rows_bytes(m0, p.M, p.lda, 2);
   const uint32_t b_bytes = (uint32_t)p.K * (uint32_t)p.ldb * 2u;
   const uint32_t wlds = lds0 + wave * 1024u;
-  const int k_rounds = (p.K - kfull * BK) / 8; // B rounds of the partial k-tile
-  const uint32_t a_kmask = a_lc < k_rounds ? 0u : kOob;
-  const u32x4 rb_none = rsrc_dwords(p.B, 0u);
   // load l of k-tile kt into ring slot ST (l is a constant once unrolled:
-  // the LDS offset becomes the literal of the M0 add). KMASK: kt may be the
-  // partial k-tile (the loop's whole-tile refills skip the masking code).
-  auto load = [&](const u32x4 &ra, const u32x4 &rb, int kt, auto st_c, int l,
-                  auto kmask_c) {
+  // the LDS offset becomes the literal of the M0 add)
+  auto load = [&](const u32x4 &ra, const u32x4 &rb, int kt, auto st_c, int l) {
     constexpr uint32_t base = decltype(st_c)::value * SLOT;
-    constexpr bool KMASK = KPART && decltype(kmask_c)::value;
-    const bool kpart = KMASK && kt == kfull; // the partial k-tile (or past the end)
     static_for<16>([&](auto l_c) {
       constexpr int L = decltype(l_c)::value;
       if (L == l) {
         if constexpr (L < 8)
-          load_lds16_at<base + L * 4096u>(
-              ra, wlds, (L * 32 < a_rows_left ? a_voff : kOob) | (kpart ? a_kmask : 0u),
-              (uint32_t)kt * a_ktile + L * a_round);
+          load_lds16_at<base + L * 4096u>(ra, wlds, L * 32 < a_rows_left ? a_voff : kOob,
+                                          (uint32_t)kt * a_ktile + L * a_round);
         else
           load_lds16_at<base + B_AT + (L - 8) * 4096u>(
-              kpart && L - 8 >= k_rounds ? rb_none : rb, wlds, (L & 1) ? b_voff1 : b_voff0,
-              (uint32_t)kt * b_ktile + (L - 8) * b_round);
+              rb, wlds, (L & 1) ? b_voff1 : b_voff0, (uint32_t)kt * b_ktile + (L - 8) * b_round);
       }
     });
   };
-  using KM = std::integral_constant<bool, true>;
-  using KW = std::integral_constant<bool, false>;
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
 
@@ -523,10 +567,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     const u32x4 rb1 = rsrc_dwords(p.B, nk > 1 ? b_bytes : 0u);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
-      load(ra, rb, 0, S0{}, l, KM{});
+      load(ra, rb, 0, S0{}, l);
 #pragma unroll
     for (int l = 0; l < 16; ++l)
-      load(ra1, rb1, 1, S1{}, l, KM{});
+      load(ra1, rb1, 1, S1{}, l);
   }
   wait_vmcnt<kMfma16VmPrologue>();
   barrier();
@@ -537,9 +581,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   kstep1(Z{}, Q{});
 
   // body(it): k-tile it (stage S) from its barrier on, k-tile it+1 (stage
-  // S^1) up to its barrier; stage S is refilled with k-tile it+2 (KMASK: the
-  // refill may be the partial k-tile).
-  auto body = [&](int it, auto stage, auto kmask_c) {
+  // S^1) up to its barrier; stage S is refilled with k-tile it+2.
+  auto body = [&](int it, auto stage) {
     constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(a_tile, ok ? a_bytes : 0u);
@@ -559,7 +602,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
           rd(0, Sn, 0, o);
       });
       if constexpr (((m - BQ) % LS) == 0)
-        load(ra, rb, it + 2, stage, (m - BQ) / LS, kmask_c);
+        load(ra, rb, it + 2, stage, (m - BQ) / LS);
       __builtin_amdgcn_sched_barrier(0);
     });
     constexpr int NB = (64 - BQ + LS - 1) / LS; // refill loads issued before k-tile it+1
@@ -567,23 +610,18 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     static_assert(OFF + (16 - NB - 1) * LS < 64, "refill fits one k-tile");
     auto refill = [&](int m) {
       if (m >= OFF && ((m - OFF) % LS) == 0 && NB + (m - OFF) / LS < 16)
-        load(ra, rb, it + 2, stage, NB + (m - OFF) / LS, kmask_c);
+        load(ra, rb, it + 2, stage, NB + (m - OFF) / LS);
     };
     kstep0(Sn, refill, false);
     kstep1(Z{}, Q{});
   };
   int it = 0;
-  if constexpr (KPART)
-    for (; it + 3 < kfull; it += 2) { // both refills are whole k-tiles
-      body(it, S0{}, KW{});
-      body(it + 1, S1{}, KW{});
-    }
   for (; it + 2 <= nk - 1; it += 2) {
-    body(it, S0{}, KM{});
-    body(it + 1, S1{}, KM{});
+    body(it, S0{});
+    body(it + 1, S1{});
   }
   if (it < nk - 1)
-    body(it, S0{}, KM{});
+    body(it, S0{});
   kstep1(Q{}, E{}); // the last k-tile after its barrier point
   // Sched::ACC_READ_WAITS (24) wait states between the last MFMA and the
   // first accumulator read
@@ -603,80 +641,75 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   // lane-derived addresses come from an opaque copy of the lane index, so the
   // compiler cannot hoist them out of a persistent tile loop and keep them
   // live in registers the main loop needs.
-  int el = lane;
-  asm volatile("" : "+v"(el));
-  const EpiArgs ea{p.bias, p.epi_bias, p.epi_act, p.epi_clamp, p.clamp_lo, p.clamp_hi};
+  int el = lane_id_fresh();
+  const GemmParams pe = params_fresh();
+  const EpiArgs ea{pe.bias, pe.epi_bias, pe.epi_act, pe.epi_clamp, pe.clamp_lo, pe.clamp_hi};
   if constexpr (OUT == kOutF16) {
     epi_f32x4 bv[EPI ? 8 : 1];
     if constexpr (EPI) { // every bias load first: one memory latency
       const int ccol = n0 + wn * 128 + 4 * (el >> 4);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        bv[j] = epi_load_bias(ea, ccol + 16 * j, p.N);
+        bv[j] = epi_load_bias(ea, ccol + 16 * j, pe.N);
     }
     barrier(); // every wave is past its last fragment read and load
     TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
     // clamp bounds: -inf / +inf for a clamp that is off
-    const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
-    const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
+    const float lo = (pe.epi_clamp & 1) ? pe.clamp_lo : -__builtin_inff();
+    const float hi = (pe.epi_clamp & 2) ? pe.clamp_hi : __builtin_inff();
     // C's window starts at row m0
     const __amdgpu_buffer_rsrc_t rc =
-        make_rsrc(rows_at(p.C, m0, p.ldc, 2), rows_bytes(m0, p.M, p.ldc, 2));
+        make_rsrc(rows_at(pe.C, m0, pe.ldc, 2), rows_bytes(m0, pe.M, pe.ldc, 2));
     const int q = el & 15;
     // One 16-row block of the wave tile at a time: its 8 tiles go into LDS,
     // then its 16 rows come back and go out, so the stores of block i run
     // while block i+1's conversions (and fused steps) execute. The region is
     // this wave's alone and a wave's LDS operations complete in order, so no
     // barrier separates a block's writes from its reads.
-    auto epilogue = [&](auto act_c, auto clamp_c) {
+    auto block = [&](auto i_c, auto act_c, auto clamp_c) {
+      constexpr int i = decltype(i_c)::value;
       constexpr int ACT = decltype(act_c)::value;
       constexpr bool CLAMP = decltype(clamp_c)::value;
+      epi_variant_fence<ACT, CLAMP>();
+      const int r = 16 * i + (el & 15);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = 16 * i + (el & 15);
+      for (int j = 0; j < 8; ++j) {
+        float x[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float x[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            x[e] = acc[i][j][e];
-            if constexpr (EPI)
-              x[e] = epi_apply_t<ACT, CLAMP>(x[e], bv[j][e], lo, hi);
-          }
-          u32x2 v;
-          v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
-          v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
-          const int chunk = (2 * j + (el >> 5)) ^ (r & 7);
-          const int half = ((el >> 4) & 1) ^ ((r >> 3) & 1);
-          *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
-          if (j & 1)
-            __builtin_amdgcn_sched_barrier(0);
+        for (int e = 0; e < 4; ++e) {
+          x[e] = acc[i][j][e];
+          if constexpr (EPI)
+            x[e] = epi_apply_t<ACT, CLAMP>(x[e], bv[j][e], lo, hi);
         }
-#pragma unroll
-        for (int t = 4 * i; t < 4 * i + 4; ++t) {
-          const int rr = t * 4 + (el >> 4); // rows 16i .. 16i+15
-          u32x4 v = *(const TBK_LDS u32x4 *)(wl + rr * 256 + ((q ^ (rr & 7)) * 16));
-          if ((rr >> 3) & 1)
-            v = (u32x4){v[2], v[3], v[0], v[1]};
-          const int row = m0 + wm * 128 + rr, col = n0 + wn * 128 + 8 * q;
-          const uint32_t off =
-              row < p.M && col < p.N
-                  ? ((uint32_t)(wm * 128 + rr) * (uint32_t)p.ldc + (uint32_t)col) * 2u
-                  : kOob;
-          // non-temporal (nt): C is written once and not read again by this
-          // kernel; measured 0.7% faster at 4096^3 than the default policy
-          __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        u32x2 v;
+        v[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[0]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[1]) << 16);
+        v[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[3]) << 16);
+        const int chunk = (2 * j + (el >> 5)) ^ (r & 7);
+        const int half = ((el >> 4) & 1) ^ ((r >> 3) & 1);
+        *(TBK_LDS u32x2 *)(wl + r * 256 + chunk * 16 + half * 8) = v;
+        if (j & 1)
+          __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int t = 4 * i; t < 4 * i + 4; ++t) {
+        const int rr = t * 4 + (el >> 4); // rows 16i .. 16i+15
+        u32x4 v = *(const TBK_LDS u32x4 *)(wl + rr * 256 + ((q ^ (rr & 7)) * 16));
+        if ((rr >> 3) & 1)
+          v = (u32x4){v[2], v[3], v[0], v[1]};
+        const int row = m0 + wm * 128 + rr, col = n0 + wn * 128 + 8 * q;
+        const uint32_t off =
+            row < pe.M && col < pe.N
+                ? ((uint32_t)(wm * 128 + rr) * (uint32_t)pe.ldc + (uint32_t)col) * 2u
+                : kOob;
+        // non-temporal (nt): C is written once and not read again by this
+        // kernel; measured 0.7% faster at 4096^3 than the default policy
+        __builtin_amdgcn_raw_buffer_store_b128(v, rc, off, 0, kStoreNT);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     };
-    // the activation and clamp are dispatched once, not per element
-    if constexpr (EPI)
-      epi_dispatch(p.epi_act, p.epi_clamp, epilogue);
-    else
-      epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+    epi_for_blocks<8, EPI>(pe, block);
   } else {
     // f32 C through LDS, one 16-row block of the wave tile at a time. Lane l
     // holds row 16i + l%16, columns 16j + 4(l/16) .. +3 of block i (16 bytes
@@ -693,11 +726,11 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     const int col = n0 + wn * 128 + 4 * q;
     // C's window starts at row m0
     const __amdgpu_buffer_rsrc_t rc =
-        make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
+        make_rsrc(rows_at(pe.C, m0, pe.ldc, 4), rows_bytes(m0, pe.M, pe.ldc, 4));
     auto c_off = [&](int i, int t) -> uint32_t {
       const int rr = wm * 128 + 16 * i + 2 * t + hr; // row of the tile
-      return m0 + rr < p.M && col < p.N
-                 ? ((uint32_t)rr * (uint32_t)p.ldc + (uint32_t)col) * 4u
+      return m0 + rr < pe.M && col < pe.N
+                 ? ((uint32_t)rr * (uint32_t)pe.ldc + (uint32_t)col) * 4u
                  : kOob;
     };
     f32x4 old[OUT == kOutF32Accum ? PF : 1][8];
@@ -712,50 +745,46 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 #pragma unroll
     for (int i = 0; i < PF; ++i)
       load_old(i);
-    const epi_f32x4 bias = EPI ? epi_load_bias(ea, col, p.N) : epi_f32x4{};
+    const epi_f32x4 bias = EPI ? epi_load_bias(ea, col, pe.N) : epi_f32x4{};
     barrier(); // every wave is past its last fragment read and load
     TBK_LDS char *wl = (TBK_LDS char *)(TBK_LDS void *)lds + wave * 32768;
-    const float lo = (p.epi_clamp & 1) ? p.clamp_lo : -__builtin_inff();
-    const float hi = (p.epi_clamp & 2) ? p.clamp_hi : __builtin_inff();
-    auto epilogue = [&](auto act_c, auto clamp_c) {
+    const float lo = (pe.epi_clamp & 1) ? pe.clamp_lo : -__builtin_inff();
+    const float hi = (pe.epi_clamp & 2) ? pe.clamp_hi : __builtin_inff();
+    auto block = [&](auto i_c, auto act_c, auto clamp_c) {
+      constexpr int i = decltype(i_c)::value;
       constexpr int ACT = decltype(act_c)::value;
       constexpr bool CLAMP = decltype(clamp_c)::value;
+      epi_variant_fence<ACT, CLAMP>();
+      TBK_LDS char *blk = wl + (i & 3) * 8192;
+      const int r = el & 15, g = el >> 4;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        TBK_LDS char *blk = wl + (i & 3) * 8192;
-        const int r = el & 15, g = el >> 4;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          *(TBK_LDS f32x4 *)(blk + r * 512 + (((4 * j + g) ^ r) * 16)) = acc[i][j];
-          if (j & 1)
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int rr = 2 * t + hr;
-          f32x4 v = *(const TBK_LDS f32x4 *)(blk + rr * 512 + ((q ^ rr) * 16));
-          if constexpr (OUT == kOutF32Accum)
-            v += old[i % PF][t];
-          if constexpr (EPI) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              v[e] = epi_apply_t<ACT, CLAMP>(v[e], bias[e], lo, hi);
-          }
-          // a plain f32 C is written once and not read again by this kernel
-          // (non-temporal); C += A*B keeps the default policy
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc,
-                                                 c_off(i, t), 0,
-                                                 OUT == kOutF32Partial ? kStoreNT : 0);
-        }
-        if (i + PF < 8)
-          load_old(i + PF);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < 8; ++j) {
+        *(TBK_LDS f32x4 *)(blk + r * 512 + (((4 * j + g) ^ r) * 16)) = acc[i][j];
+        if (j & 1)
+          __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int rr = 2 * t + hr;
+        f32x4 v = *(const TBK_LDS f32x4 *)(blk + rr * 512 + ((q ^ rr) * 16));
+        if constexpr (OUT == kOutF32Accum)
+          v += old[i % PF][t];
+        if constexpr (EPI) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = epi_apply_t<ACT, CLAMP>(v[e], bias[e], lo, hi);
+        }
+        // a plain f32 C is written once and not read again by this kernel
+        // (non-temporal); C += A*B keeps the default policy
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc,
+                                               c_off(i, t), 0,
+                                               OUT == kOutF32Partial ? kStoreNT : 0);
+      }
+      if (i + PF < 8)
+        load_old(i + PF);
+      __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (EPI)
-      epi_dispatch(p.epi_act, p.epi_clamp, epilogue);
-    else
-      epilogue(std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+    epi_for_blocks<8, EPI>(pe, block);
   }
 }
 
@@ -1593,7 +1622,7 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
 
 // The programs of the 16x16x32 instance of the 4-wave 256x256x64 2-stage
 // configuration (any M, N and K; tile, grouped or persistent order).
-template <int OUT, bool EPI, bool KPART>
+template <int OUT, bool EPI>
 __device__ __forceinline__ void mfma16_programs(const GemmParams &p, u32x4 *lds) {
   const bool persistent =
       p.mapping == kMapPersistent || p.mapping == kMapPersistentGrouped;
@@ -1607,22 +1636,22 @@ __device__ __forceinline__ void mfma16_programs(const GemmParams &p, u32x4 *lds)
     map_program(p, work, tile_m, tile_n, part);
     if (work != prog)
       __syncthreads(); // every wave read its staged epilogue back
-    mfma16_tile<OUT, EPI, KPART>(p, tile_m * 256, tile_n * 256, lds);
+    mfma16_tile<OUT, EPI>(p, tile_m * 256, tile_n * 256, lds);
   }
 }
 
 // f16 C
-template <bool EPI, bool KPART>
+template <bool EPI>
 __global__ __launch_bounds__(256, 1) void gemm_mfma16(GemmParams p) {
   __shared__ u32x4 lds[8192]; // the 2-stage ring of 256x64 + 64x256 halves
-  mfma16_programs<kOutF16, EPI, KPART>(p, lds);
+  mfma16_programs<kOutF16, EPI>(p, lds);
 }
 
 // f32 C: a plain store (OUT = kOutF32Partial) or C += A*B (kOutF32Accum)
-template <int OUT, bool EPI, bool KPART>
+template <int OUT, bool EPI>
 __global__ __launch_bounds__(256, 1) void gemm_mfma16_f32(GemmParams p) {
   __shared__ u32x4 lds[8192];
-  mfma16_programs<OUT, EPI, KPART>(p, lds);
+  mfma16_programs<OUT, EPI>(p, lds);
 }
 
 } // namespace tbk

@@ -155,3 +155,47 @@
   X(192, 128, 64, 2, 2, 3), X(192, 128, 64, 2, 2, 4), \
   X(192, 128, 64, 2, 4, 2), X(192, 128, 64, 2, 4, 3), \
   X(192, 128, 64, 2, 4, 4)
+
+// ---- the 16x16x32 loop (gemm_mfma16g.h) ------------------------------------
+// Tiles built on v_mfma_f32_16x16x32_f16 besides the hand-scheduled 4-wave
+// 256x256x64 2-stage instance, as (BM, BN, BK, wave grid M, wave grid N,
+// LDS stages), one list per block shape (the Makefile compiles each list
+// plain and with the fused epilogue steps, in the f16, plain f32 and
+// f32 C += A*B modes). Wave tiles hold 16..64 MFMA tiles of 16x16 (at most
+// 256 accumulator registers); the wave grid is the one the plan derives.
+// (The hand-scheduled tile's partial-K build is this loop too, instantiated
+// with its entries. 8 waves of 64x128 on 256x256 do not fit their 256
+// registers per wave and are not listed.) The lists cover the 4- and 8-wave
+// picks of the common blocks, and at block_k 64
+// the wave tiles of 128x128 (1 wave on 128x128, 2 on 256x128 / 128x256),
+// 256x64 (1 wave) and 96x128 (2 waves on 192x128) whose 32x32x16 builds
+// spill. Wave tiles of 48 or 64 MFMA tiles are listed at block_k 64 only:
+// with 32-deep k-tiles the fragment buffer of the last k-tile depends on
+// the k-tile count's parity, and with 192-256 accumulator registers held
+// the compiler spills at the two tails' merge.
+#define TBK_M16_SHAPES(S) S(128x128) S(256x128) S(128x256) S(256x64) S(192x128)
+
+#define TBK_M16_TILES_128x128(X) \
+  X(128, 128, 64, 2, 2, 2), X(128, 128, 64, 2, 2, 3), X(128, 128, 64, 2, 2, 4), \
+  X(128, 128, 32, 2, 2, 2), X(128, 128, 32, 2, 2, 3), X(128, 128, 32, 2, 2, 4), \
+  X(128, 128, 64, 1, 1, 2)
+
+#define TBK_M16_TILES_256x128(X) \
+  X(256, 128, 64, 4, 1, 2), X(256, 128, 64, 4, 1, 3), \
+  X(256, 128, 32, 4, 1, 2), X(256, 128, 32, 4, 1, 3), X(256, 128, 32, 4, 1, 4), \
+  X(256, 128, 64, 4, 2, 2), X(256, 128, 64, 4, 2, 3), \
+  X(256, 128, 64, 2, 1, 2), X(256, 128, 64, 2, 1, 3)
+
+#define TBK_M16_TILES_128x256(X) \
+  X(128, 256, 64, 1, 4, 2), X(128, 256, 64, 1, 4, 3), \
+  X(128, 256, 32, 1, 4, 2), X(128, 256, 32, 1, 4, 3), X(128, 256, 32, 1, 4, 4), \
+  X(128, 256, 64, 2, 4, 2), X(128, 256, 64, 2, 4, 3), \
+  X(128, 256, 64, 1, 2, 2), X(128, 256, 64, 1, 2, 3)
+
+
+#define TBK_M16_TILES_256x64(X) X(256, 64, 64, 1, 1, 2)
+
+#define TBK_M16_TILES_192x128(X) \
+  X(192, 128, 64, 2, 1, 2), X(192, 128, 64, 2, 1, 3), X(192, 128, 64, 2, 1, 4), \
+  X(192, 128, 64, 2, 2, 2), X(192, 128, 64, 2, 2, 3), X(192, 128, 64, 2, 2, 4), \
+  X(192, 128, 32, 2, 2, 2), X(192, 128, 32, 2, 2, 3), X(192, 128, 32, 2, 2, 4)

@@ -43,6 +43,8 @@ const Attr &need(const Op &op, const char *attr, const char *producer) {
 KernelConfig checkedConfig(const Module &m, const Op &op, const TargetInfo *t) {
   KernelConfig c = getKernelConfig(m, op);
   verifySupportedKernelConfig(c, t);
+  if (t) // with the gfx950 target: the bound instance holds its registers
+    verifyInstanceRegisters(m, op, c);
   return c;
 }
 

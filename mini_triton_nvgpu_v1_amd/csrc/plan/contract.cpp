@@ -293,6 +293,9 @@ tb_gemm_config lowerContractToConfig(const KernelContract &k) {
   if (!hasGfx950Instance(key))
     throw Error("no gfx950 kernel instance `" + instanceName(key) +
                 "` for this contract (see tb-opt --list-instances)");
+  // register truth: the compiler's report of the instance (build-time table)
+  if (const std::string why = spillRefusal(key, g.k % g.block_k != 0); !why.empty())
+    throw Error(why);
   checkKernelWaits(k, key);
   return g;
 }

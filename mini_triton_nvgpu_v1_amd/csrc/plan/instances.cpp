@@ -24,8 +24,41 @@ struct Tile {
 #define TB_SHAPE_TILES(SHAPE) TBK_TILES_##SHAPE(TB_TILE),
 const Tile kTiles[] = {TBK_SHAPES(TB_SHAPE_TILES)};
 #undef TB_SHAPE_TILES
+// the 16x16x32 loop's tiles (besides the hand-scheduled 256x256x64 one)
+#define TB_M16_SHAPE_TILES(SHAPE) TBK_M16_TILES_##SHAPE(TB_TILE),
+const Tile kM16Tiles[] = {TBK_M16_SHAPES(TB_M16_SHAPE_TILES)};
+#undef TB_M16_SHAPE_TILES
 #undef TB_TILE
+
+// the hand-scheduled 16x16x32 instance: 4 waves of 128x128 on 256x256x64, 2 stages
+bool handScheduled16(int64_t bm, int64_t bn, int64_t bk, int64_t wgm, int64_t wgn,
+                     int64_t stages) {
+  return bm == 256 && bn == 256 && bk == 64 && wgm == 2 && wgn == 2 && stages == 2;
+}
+
+// Mfma16GTile's issue schedule, restated (gemm_mfma16g.h): loads per thread,
+// the refill's spread over the MFMA slots of a loop body
+struct M16Geometry {
+  int64_t lpt, spread;
+};
+M16Geometry m16Geometry(const InstanceKey &k) {
+  const int64_t nt = k.wgm * k.wgn * 64;
+  const int64_t lpt = (k.bm * k.bk * 2 + k.bk * k.bn * 2) / (nt * 16);
+  const int64_t nm = (k.bm / k.wgm / 16) * (k.bn / k.wgn / 16), nslot = (k.bk / 32) * nm;
+  return {lpt, k.stages == 2 ? nslot * 5 / 8 : nslot - nslot / 8};
+}
 } // namespace
+
+bool hasMfma16Tile(int64_t bm, int64_t bn, int64_t bk, int64_t wgm, int64_t wgn,
+                   int64_t stages) {
+  if (handScheduled16(bm, bn, bk, wgm, wgn, stages))
+    return true;
+  for (const Tile &t : kM16Tiles)
+    if (t.bm == bm && t.bn == bn && t.bk == bk && t.wgm == wgm && t.wgn == wgn &&
+        t.stages == stages)
+      return true;
+  return false;
+}
 
 const std::vector<InstanceKey> &gfx950Instances() {
   static const std::vector<InstanceKey> all = [] {
@@ -37,10 +70,15 @@ const std::vector<InstanceKey> &gfx950Instances() {
       for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
         v.push_back({t.bm, t.bn, t.bk, t.wgm, t.wgn, out, t.stages, 1, TB_MFMA_32X32X16});
     }
-    // 16x16x32: f16 C, plain f32 C and f32 C += A*B (no split-K)
+    // 16x16x32: f16 C, plain f32 C and f32 C += A*B (no split-K), the
+    // hand-scheduled 256x256x64 tile and the 16x16x32 loop's tiles
     for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
       for (int epi = 0; epi <= 1; ++epi)
         v.push_back({256, 256, 64, 2, 2, out, 2, epi, TB_MFMA_16X16X32});
+    for (const Tile &t : kM16Tiles)
+      for (int epi = 0; epi <= 1; ++epi)
+        for (int out = kInstOutF16; out <= kInstOutF32Accum; ++out)
+          v.push_back({t.bm, t.bn, t.bk, t.wgm, t.wgn, out, t.stages, epi, TB_MFMA_16X16X32});
     return v;
   }();
   return all;
@@ -93,6 +131,20 @@ static bool producerTile(const InstanceKey &k) {
 
 InstanceSchedule instanceSchedule(const InstanceKey &k) {
   InstanceSchedule s;
+  if (k.mfma == TB_MFMA_16X16X32 && !handScheduled16(k.bm, k.bn, k.bk, k.wgm, k.wgn, k.stages)) {
+    // the 16x16x32 loop: the prologue issues every stage's k-tile whole;
+    // each barrier waits for the next k-tile and for this wave's LDS reads,
+    // then the freed stage is refilled, its loads spread over the body
+    const M16Geometry g = m16Geometry(k);
+    s.issue = "tile16_slots";
+    s.loadsPerThread = g.lpt;
+    s.prologueTailLoads = g.lpt;
+    s.refillSpreadSlots = g.spread;
+    s.vmPrologue = (k.stages - 1) * g.lpt;
+    s.vmLoop = (k.stages - 2) * g.lpt;
+    s.lgkmLoop = 0;
+    return s;
+  }
   if (k.mfma == TB_MFMA_16X16X32) {
     s.issue = "exact_tile_slots";
     s.loadsPerThread = 16; // 256x64 + 64x256 halves, 16-byte loads, 256 lanes
@@ -132,6 +184,82 @@ InstanceSchedule instanceSchedule(const InstanceKey &k) {
   s.vmLoop = (k.stages - 2) * lpt;
   s.lgkmLoop = -1;
   return s;
+}
+
+namespace {
+struct ResourceRow {
+  const char *family;
+  std::vector<int> args;
+  int vgprs, agprs, sgprs, scratch;
+};
+const ResourceRow kResources[] = {
+#include "instance_resources.inc"
+};
+
+// The rows of the builds key k binds: the general loop's gemm_kernel (or the
+// producer-wave build that replaces its f32-partial entry), or the 16x16x32
+// instance with its partial-K build.
+bool rowBinds(const ResourceRow &r, const InstanceKey &k, bool partialK) {
+  const std::string f = r.family;
+  const auto &a = r.args;
+  if (k.mfma == TB_MFMA_16X16X32) {
+    // the hand-scheduled tile runs whole k-tiles; a partial last k-tile
+    // runs the 16x16x32 loop's build of the same tile
+    if (handScheduled16(k.bm, k.bn, k.bk, k.wgm, k.wgn, k.stages) && !partialK) {
+      if (f == "gemm_mfma16" && k.out == kInstOutF16)
+        return a.size() == 1 && a[0] == k.epi;
+      if (f == "gemm_mfma16_f32" && k.out != kInstOutF16)
+        return a.size() == 2 && a[0] == k.out && a[1] == k.epi;
+      return false;
+    }
+    return f == "gemm_mfma16g" && a.size() == 8 && a[0] == k.bm && a[1] == k.bn &&
+           a[2] == k.bk && a[3] == k.wgm && a[4] == k.wgn && a[5] == k.stages &&
+           a[6] == k.out && a[7] == k.epi;
+  }
+  if (k.out == kInstOutF32Partial && !k.epi && producerTile(k))
+    return f == "gemm_kernel_pw" && a.size() == 6 && a[0] == k.bm && a[1] == k.bn &&
+           a[2] == k.bk && a[3] == k.wgm && a[4] == k.wgn && a[5] == k.stages;
+  return f == "gemm_kernel" && a.size() == 9 && a[0] == k.bm && a[1] == k.bn &&
+         a[2] == k.bk && a[3] == k.wgm && a[4] == k.wgn && a[5] == k.out &&
+         a[6] == k.stages && a[8] == k.epi;
+}
+
+std::string familyName(const ResourceRow &r) {
+  std::string s = std::string(r.family) + "<";
+  for (size_t i = 0; i < r.args.size(); ++i)
+    s += (i ? ", " : "") + std::to_string(r.args[i]);
+  return s + ">";
+}
+} // namespace
+
+InstanceResources instanceResources(const InstanceKey &k, bool partialK) {
+  InstanceResources res;
+  for (const ResourceRow &r : kResources) {
+    if (!rowBinds(r, k, partialK))
+      continue;
+    if (!res.known || r.scratch > res.scratchBytes ||
+        (r.scratch == res.scratchBytes && r.vgprs + r.agprs > res.vgprs + res.agprs))
+      res.kernel = familyName(r);
+    res.known = true;
+    res.vgprs = std::max<int64_t>(res.vgprs, r.vgprs);
+    res.agprs = std::max<int64_t>(res.agprs, r.agprs);
+    res.sgprs = std::max<int64_t>(res.sgprs, r.sgprs);
+    res.scratchBytes = std::max<int64_t>(res.scratchBytes, r.scratch);
+  }
+  return res;
+}
+
+std::string spillRefusal(const InstanceKey &k, bool partialK) {
+  const InstanceResources r = instanceResources(k, partialK);
+  if (!r.known || r.scratchBytes == 0)
+    return "";
+  return "gfx950 kernel instance " + instanceName(k) +
+         (partialK ? " (its build for a partial last k-tile)" : "") + " spills " +
+         std::to_string(r.scratchBytes) + " bytes per lane to scratch (" +
+         std::to_string(r.vgprs) + " VGPRs, " + std::to_string(r.agprs) +
+         " AGPRs per wave, compiler report of " + r.kernel +
+         "): the wave tile does not fit the registers of one wave; use more waves or a "
+         "smaller block";
 }
 
 std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>

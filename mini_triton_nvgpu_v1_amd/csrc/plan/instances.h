@@ -54,8 +54,13 @@ int instanceOutOf(bool splitK, bool atomicReduction, bool f16C, bool loadC);
 //    S-1 (those a refill issues before the next barrier);
 //  * "burst": smaller wave tiles; a refill is issued whole right after the
 //    barrier, and the prologue issues all S k-tiles;
-//  * "exact_tile_slots": the 16x16x32 instance (k-tiles 0 and 1 whole in the
-//    prologue; every barrier waits for all loads and LDS reads);
+//  * "exact_tile_slots": the hand-scheduled 16x16x32 instance (k-tiles 0 and
+//    1 whole in the prologue; every barrier waits for all loads and LDS
+//    reads);
+//  * "tile16_slots": the 16x16x32 loop of the other tiles (all S k-tiles
+//    whole in the prologue; each barrier waits for the next k-tile and, with
+//    lgkmcnt(0), for the wave's LDS reads; the refill of the freed stage is
+//    spread over `refillSpreadSlots` MFMA slots);
 //  * "producer_waves": the f32-partial tiles of TBK_PRODUCER_TILES, whose
 //    workgroup adds `loaderWaves` waves that only issue the loads: they issue
 //    all S k-tiles in the prologue and, at each barrier, wait for the next
@@ -70,6 +75,29 @@ struct InstanceSchedule {
   int64_t loaderWaves = 0; // load-only waves beside the wave grid's
 };
 InstanceSchedule instanceSchedule(const InstanceKey &k);
+
+// The compiler's register and scratch report for the build an instance key
+// binds (the build step reads hipcc's kernel-resource-usage remarks into the
+// table; csrc/tools/resource_table.py): VGPRs, AGPRs and SGPRs per wave and
+// scratch bytes per lane. `partialK`: the problem's K is not a multiple of
+// block_k, which the hand-scheduled 16x16x32 instance serves with the
+// 16x16x32 loop's build of its tile (every other instance has one build for
+// all K). `known` is false for a key with no compiled kernel.
+struct InstanceResources {
+  bool known = false;
+  int64_t vgprs = 0, agprs = 0, sgprs = 0, scratchBytes = 0;
+  std::string kernel; // the kernel function the numbers come from
+};
+InstanceResources instanceResources(const InstanceKey &k, bool partialK = false);
+// The refusal of an instance that spills ("" when it does not): the plan
+// binds only instances whose registers hold the whole wave tile.
+std::string spillRefusal(const InstanceKey &k, bool partialK = false);
+
+// A 16x16x32 instance exists for this block, wave grid and stage count (in
+// every output mode, plain and fused): the hand-scheduled 256x256x64 tile
+// or a tile of TBK_M16_SHAPES.
+bool hasMfma16Tile(int64_t bm, int64_t bn, int64_t bk, int64_t wgm, int64_t wgn,
+                   int64_t stages);
 
 // (wave grid, stages) pairs compiled for a block shape on 32x32x16 MFMA.
 std::vector<std::pair<std::pair<int64_t, int64_t>, int64_t>>

@@ -90,6 +90,11 @@ const char *mmaKindName(MmaKind k);
 int64_t scalarBytes(ScalarKind k);
 KernelConfig getKernelConfig(const Module &m, const Op &matmul);
 void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t);
+// Register truth at KernelConfig legality: the instance a tb.matmul binds
+// (its output mode and fused steps follow from the module's split-k and
+// reduction attrs, C's type and the op's epilogue attrs) must not spill
+// to scratch in the compiler's report of its build.
+void verifyInstanceRegisters(const Module &m, const Op &op, const KernelConfig &c);
 // The wave grid the EncodingPlan derives (reference EncodingPlan.cpp:283-320):
 // minimal |wave_tile_m - wave_tile_n| over grids of whole instrM x instrN
 // tiles, ties to more waves along the longer block side.

@@ -157,15 +157,23 @@ static int64_t opI64(const Op &op, const char *name, bool required, int64_t dflt
   return it->second->i;
 }
 
-// gfx950: the v_mfma_f32_16x16x32_f16 instances exist for the 4-wave
-// 256x256x64 2-stage tile (the plan's 2x2 wave grid of 128x128 wave tiles)
-// with an f16 C, a plain f32 C or f32 C += A*B, any M, N and K (they mask
-// ragged edges). Per FLOP it moves a quarter of the accumulator register
-// traffic of 32x32x16, which this power-limited part turns into a higher
-// sustained clock. (Split-K has no 16x16x32 instance: the caller checks.)
+// gfx950: v_mfma_f32_16x16x32_f16 instances exist for the 4-wave
+// 256x256x64 2-stage tile (hand-scheduled) and for the tiles of the
+// 16x16x32 loop (kernels/gemm_tiles.h, TBK_M16_TILES_*), on the wave grid
+// the plan derives, with an f16 C, a plain f32 C or f32 C += A*B, plain or
+// fused, any M, N and K (they mask ragged edges). Per FLOP it moves a
+// quarter of the accumulator register traffic of 32x32x16, which this
+// power-limited part turns into a higher sustained clock, and its wave
+// tiles of 128x128 (and 256x64, 96x128) hold their accumulators without
+// spilling. (Split-K has no 16x16x32 instance: the caller checks.)
 bool mfma16x16x32Supported(const KernelConfig &c) {
-  return c.blockM == 256 && c.blockN == 256 && c.blockK == 64 && c.numWarps == 4 &&
-         c.requestedStages == 2;
+  std::pair<int64_t, int64_t> g;
+  try {
+    g = deriveWaveGrid(c, 32, 32);
+  } catch (const Error &) {
+    return false;
+  }
+  return hasMfma16Tile(c.blockM, c.blockN, c.blockK, g.first, g.second, c.requestedStages);
 }
 
 // Reference: KernelConfig.cpp:86-132 (tb.matmul) and the post-cleanup
@@ -262,6 +270,40 @@ static void verifyCompiledInstance(const KernelConfig &c) {
               "and stages for this block: " + (have.empty() ? "none" : have));
 }
 
+void verifyInstanceRegisters(const Module &m, const Op &op, const KernelConfig &c) {
+  if (op.name != "tb.matmul")
+    return; // past the rewrite the lowering checks the exact instance
+  std::pair<int64_t, int64_t> g;
+  try {
+    g = deriveWaveGrid(c, 32, 32);
+  } catch (const Error &) {
+    return; // the encoding plan reports the missing wave grid
+  }
+  const bool splitK = moduleI64(m, kSplitK, false, 1) > 1;
+  bool atomic = false;
+  if (AttrP a = m.attr(kReductionMode))
+    atomic = a->kind == AttrKind::String && a->s == "split_k_parallel";
+  const bool f16C = c.cScalar == ScalarKind::F16;
+  bool fused = false;
+  for (const char *name : {"epilogue_bias", "epilogue_activation", "epilogue_clamp_min",
+                           "epilogue_clamp_max"})
+    fused = fused || op.attrs.count(name) != 0;
+  InstanceKey key;
+  key.bm = c.blockM;
+  key.bn = c.blockN;
+  key.bk = c.blockK;
+  key.wgm = g.first;
+  key.wgn = g.second;
+  key.stages = c.requestedStages;
+  key.out = instanceOutOf(splitK, splitK && atomic, f16C, !f16C);
+  key.epi = fused && !splitK ? 1 : 0;
+  key.mfma = c.mmaKind == MmaKind::Mfma16x16x32F16 ? TB_MFMA_16X16X32 : TB_MFMA_32X32X16;
+  if (!hasGfx950Instance(key))
+    return; // the lowering names the missing instance
+  if (const std::string why = spillRefusal(key, c.problemK % c.blockK != 0); !why.empty())
+    throw Error(why);
+}
+
 // Reference: KernelConfig.cpp:202-246. gfx950 legality: f16 x f16 into an
 // f16 or f32 C through v_mfma_f32_32x32x16_f16, so the block shape must be
 // a multiple of the MFMA tile (32 x 32, k 16) and block_k one or two
@@ -273,8 +315,8 @@ void verifySupportedKernelConfig(const KernelConfig &c, const TargetInfo *t) {
     throw Error("gfx950 stage1 supports mma = `mfma_f32_32x32x16_f16` or "
                 "`mfma_f32_16x16x32_f16`");
   if (c.mmaKind == MmaKind::Mfma16x16x32F16 && !mfma16x16x32Supported(c))
-    throw Error("mma = `mfma_f32_16x16x32_f16` is implemented for the 4-wave "
-                "256x256x64 2-stage tile only");
+    throw Error("mma = `mfma_f32_16x16x32_f16` has no gfx950 kernel instance for "
+                "this block, wave count and stage count (see tb-opt --list-instances)");
   if (c.problemM <= 0 || c.problemN <= 0 || c.problemK <= 0)
     throw Error("problem M/N/K must be positive");
   if (c.blockM <= 0 || c.blockN <= 0 || c.blockK <= 0)

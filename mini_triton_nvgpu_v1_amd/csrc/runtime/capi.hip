@@ -10,6 +10,7 @@
 #include "tb_gfx950.h"
 
 #include "../kernels/gemm_gfx950.h"
+#include "../plan/instances.h"
 #include "desc.h"
 
 #include <hip/hip_runtime.h>
@@ -167,6 +168,22 @@ int create_desc(const tb_gemm_config &c, tb_gemm_desc **out) {
                      (int)c.wave_grid_m, (int)c.wave_grid_n, out_mode,
                      (int)c.stages, epi, (int)c.mfma};
   const tbk::KernelEntry *e = tbk::find_kernel(key);
+  // an instance that spills to scratch is refused, as the plan refuses it
+  // (the build-time table of the compiler's register report)
+  if (e) {
+    tb::InstanceKey ik;
+    ik.bm = c.block_m;
+    ik.bn = c.block_n;
+    ik.bk = c.block_k;
+    ik.wgm = c.wave_grid_m;
+    ik.wgn = c.wave_grid_n;
+    ik.out = out_mode;
+    ik.stages = c.stages;
+    ik.epi = epi;
+    ik.mfma = c.mfma;
+    if (const std::string why = tb::spillRefusal(ik, c.k % c.block_k != 0); !why.empty())
+      return fail(why);
+  }
   if (!e) {
     char buf[256];
     snprintf(buf, sizeof buf,
@@ -412,14 +429,17 @@ int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
                    "hipLaunchKernel(fill)");
 }
 
-int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream) {
+int tb_clock_probe(uint64_t *out, int32_t workgroups, int32_t window_ticks, void *stream) {
   if (!out || workgroups < 1 || workgroups > 1024)
-    return fail("tb_clock_stamp: out must be a device pointer and workgroups in 1..1024");
+    return fail("tb_clock_probe: out must be a device pointer and workgroups in 1..1024");
+  if (window_ticks < 1 || window_ticks > 100000)
+    return fail("tb_clock_probe: window_ticks must be in 1..100000 (1 ms)");
   if (reinterpret_cast<uintptr_t>(out) % 8)
-    return fail("tb_clock_stamp: out must be 8-byte aligned");
-  return check_hip(tbk::launch_clock_stamp(reinterpret_cast<unsigned long long *>(out),
-                                           workgroups, reinterpret_cast<hipStream_t>(stream)),
-                   "hipLaunchKernel(clock stamp)");
+    return fail("tb_clock_probe: out must be 8-byte aligned");
+  return check_hip(tbk::launch_clock_probe(reinterpret_cast<unsigned long long *>(out),
+                                           workgroups, (unsigned)window_ticks,
+                                           reinterpret_cast<hipStream_t>(stream)),
+                   "hipLaunchKernel(clock probe)");
 }
 
 int tb_kernel_count(void) { return tbk::kernel_count(); }

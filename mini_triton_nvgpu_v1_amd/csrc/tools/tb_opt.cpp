@@ -37,7 +37,8 @@ void usage() {
               "[--pass-pipeline='builtin.module(...)'] [--<pass>[=<options>]]...\n"
               "       tb-opt --list-passes\n"
               "       tb-opt --list-instances   (the gfx950 kernels a plan can bind, with the\n"
-              "                                  issue schedule and waits the plan states)\n");
+              "                                  issue schedule and waits the plan states and\n"
+              "                                  the compiled registers and scratch bytes)\n");
 }
 
 } // namespace
@@ -58,13 +59,20 @@ int main(int argc, char **argv) {
         return 0;
       }
       if (a == "--list-instances") {
-        // name, then the s_waitcnt depths the plan states for it
+        // name, the s_waitcnt depths the plan states for it, and the
+        // compiler's register and scratch report of its build
         for (const tb::InstanceKey &k : tb::gfx950Instances()) {
           const tb::InstanceSchedule s = tb::instanceSchedule(k);
+          const tb::InstanceResources r = tb::instanceResources(k);
+          const tb::InstanceResources rk = tb::instanceResources(k, true);
           std::printf("%s %s vmcnt_prologue=%lld vmcnt_loop=%lld lgkmcnt_loop=%lld "
-                      "loader_waves=%lld\n",
+                      "loader_waves=%lld vgprs=%lld agprs=%lld scratch=%lld "
+                      "scratch_partial_k=%lld\n",
                       tb::instanceName(k).c_str(), s.issue.c_str(), (long long)s.vmPrologue,
-                      (long long)s.vmLoop, (long long)s.lgkmLoop, (long long)s.loaderWaves);
+                      (long long)s.vmLoop, (long long)s.lgkmLoop, (long long)s.loaderWaves,
+                      (long long)r.vgprs, (long long)r.agprs,
+                      r.known ? (long long)r.scratchBytes : -1LL,
+                      rk.known ? (long long)rk.scratchBytes : -1LL);
         }
         return 0;
       }

@@ -68,12 +68,13 @@ def _wide(**kw):
 
 def test_mfma_16x16x32_instance_selection():
     """The 4-wave 256x256x64 f16 config binds the 16x16x32 instance when the
-    config asks for it; 32x32x16 stays available for the same tile."""
+    config asks for it; its 32x32x16 build spills (128x128 wave tiles of 32x32
+    MFMA tiles) and is refused with the compiler's figures."""
     assert configs.ROOFLINE.direct_config().mfma == tb.MFMA_16X16X32
     d16 = tb.GemmDesc.from_config(_wide())
     assert d16.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"
-    d32 = tb.GemmDesc.from_config(_wide(mfma=tb.MFMA_32X32X16))
-    assert d32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out0"
+    with pytest.raises(tb.TbError, match=r"_out0 spills \d+ bytes per lane to scratch"):
+        tb.GemmDesc.from_config(_wide(mfma=tb.MFMA_32X32X16))
     fused = tb.GemmDesc.from_config(_wide(epi_activation=tb.ACT_RELU))
     assert fused.kernel_name.endswith("_16x16x32_epi")
     plain32 = tb.GemmDesc.from_config(_wide(c_dtype=tb.DTYPE_F32))

@@ -12,8 +12,10 @@ def test_plan_derivations(tmp_path):
     sources = sorted(str(p) for d in ("ir", "plan", "passes")
                      for p in (PKG / "csrc" / d).glob("*.cpp"))
     exe = tmp_path / "test_plans"
+    # instances.cpp includes the build's instance resource table (_build/)
     build = subprocess.run(["g++", "-std=c++17", "-O0", f"-I{PKG / 'csrc'}",
-                            f"-I{PKG.parent / 'include'}", str(SRC), *sources, "-o", str(exe)],
+                            f"-I{PKG / '_build'}", f"-I{PKG.parent / 'include'}", str(SRC),
+                            *sources, "-o", str(exe)],
                            capture_output=True, text=True, timeout=600)
     assert build.returncode == 0, build.stderr[-3000:]
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)

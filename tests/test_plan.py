@@ -158,7 +158,7 @@ ERRORS = [
      FULL, "needs an f32 C"),
     ("wave_grid", matmul_module(warps=3), FULL, "legal wave grid"),
     ("mfma16_small_tile", matmul_module(extra_op=', mma = "mfma_f32_16x16x32_f16"'),
-     FULL, "implemented for the 4-wave 256x256x64 2-stage tile"),
+     FULL, "has no gfx950 kernel instance for this block"),
     ("mfma16_split_k", matmul_module(
         M=256, N=256, K=256, bm=256, bn=256, bk=64,
         extra_module=', "tb.split-k" = 2 : i64',
@@ -192,24 +192,33 @@ def test_plan_from_mlir_diagnostics(name, text, arg, msg):
 
 def test_mfma_instruction_choice():
     """Without an `mma` attribute the plan takes 16x16x32 exactly where that
-    instance exists: the 4-wave 256x256x64 2-stage tile with an f16 C or an
-    f32 C (C += A*B, the reference's semantics), M, N and K possibly ragged,
-    without split-K. The EncodingPlan records the instruction shape."""
+    instance exists: the hand-scheduled 4-wave 256x256x64 2-stage tile and
+    the 16x16x32 loop's tiles (here 4 waves on 128x128 and 256x128, 2 on
+    256x128), with an f16 C or an f32 C (C += A*B, the reference's
+    semantics), M, N and K possibly ragged, without split-K. Elsewhere it
+    takes 32x32x16, and it refuses a 32x32x16 build that spills. The
+    EncodingPlan records the instruction shape."""
     def launch(text):
         return tb.plan_from_mlir(text)
     wide = dict(M=512, N=768, K=192, bm=256, bn=256, bk=64)
     assert launch(matmul_module(**wide)).config.mfma == tb.MFMA_16X16X32
     for kw in (dict(wide, M=520, N=200, exact=False), dict(wide, K=200, exact=False),
-               dict(wide, c="f32"), dict(wide, c="f32", M=520, K=200, exact=False)):
+               dict(wide, c="f32"), dict(wide, c="f32", M=520, K=200, exact=False),
+               dict(wide, bm=128, bn=128), dict(wide, bn=128, bk=32, stages=3),
+               dict(wide, bn=128, warps=2), dict(wide, bm=128, bn=128, warps=1)):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_16X16X32, kw
     f32 = tb.plan_from_mlir(matmul_module(**dict(wide, c="f32")))
     assert f32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out2_16x16x32"
-    for kw in (dict(wide, warps=8), dict(wide, bk=32),
+    for kw in (dict(wide, warps=8),
                dict(wide, extra_module=', "tb.split-k" = 3 : i64'),
                dict(wide, c="f32", extra_module=', "tb.split-k" = 2 : i64, '
-                    '"tb.reduction-mode" = "split_k_parallel"'),
-               dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"'), {}):
+                    '"tb.reduction-mode" = "split_k_parallel"'), {}):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_32X32X16, kw
+    # 32x32x16 builds of 128x128 wave tiles spill: refused at KernelConfig
+    # legality with the compiler's figures
+    for kw in (dict(wide, bk=32), dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"')):
+        with pytest.raises(tb.TbError, match=r"tb-build-program-mapping-plan: .* spills"):
+            launch(matmul_module(**kw))
     text = tb_opt(matmul_module(**wide), f"--pass-pipeline={MAINLINE}").stdout
     assert "instrShape = [16, 16, 32]" in text
     text = tb_opt(matmul_module(), f"--pass-pipeline={MAINLINE}").stdout
@@ -383,10 +392,12 @@ def test_ir_type_and_op_verifiers():
     assert p.returncode == 1 and "requires module attr `tb.num-ctas`" in p.stderr
 
 
-def _listed_instances(loader_waves=False):
+def _listed_instances(loader_waves=False, resources=False):
     """tb-opt --list-instances: name -> (issue schedule, vmcnt prologue,
     vmcnt loop, lgkmcnt loop) from the host-side table; with loader_waves,
-    name -> the load-only waves the instance adds to its wave grid."""
+    name -> the load-only waves the instance adds to its wave grid; with
+    resources, name -> (VGPRs, AGPRs, scratch bytes per lane) of the
+    compiler's report."""
     p = subprocess.run([str(TB_OPT), "--list-instances"], capture_output=True,
                        text=True, timeout=60, check=True)
     out = {}
@@ -394,9 +405,12 @@ def _listed_instances(loader_waves=False):
         name, issue, *kv = line.split()
         vals = dict(x.split("=") for x in kv)
         assert name not in out
-        out[name] = int(vals["loader_waves"]) if loader_waves else (
-            issue, int(vals["vmcnt_prologue"]), int(vals["vmcnt_loop"]),
-            int(vals["lgkmcnt_loop"]))
+        if resources:
+            out[name] = (int(vals["vgprs"]), int(vals["agprs"]), int(vals["scratch"]))
+        else:
+            out[name] = int(vals["loader_waves"]) if loader_waves else (
+                issue, int(vals["vmcnt_prologue"]), int(vals["vmcnt_loop"]),
+                int(vals["lgkmcnt_loop"]))
     return out
 
 
@@ -425,7 +439,7 @@ def test_tb_opt_instance_table_equals_the_kernel_registry():
         assert (vmp, vml, lgkm) == compiled[name], (name, issue)
     # the four issue schedules all occur, and differ in the prologue wait
     assert {v[0] for v in listed.values()} == {"slot_spread", "burst", "exact_tile_slots",
-                                               "producer_waves"}
+                                               "producer_waves", "tile16_slots"}
     assert listed["tb_gemm_gfx950_256x256x64_w4x2_s2_out0"][1:] == (4, 0, -1)
     assert listed["tb_gemm_gfx950_128x64x64_w4x1_s3_out1"][:2] == ("burst", 12)
     assert listed["tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"][1:] == (16, 0, 0)
@@ -505,6 +519,14 @@ SWEEP_BLOCKS = [(64, 64), (64, 128), (128, 64), (128, 128), (64, 256), (256, 64)
                 (128, 256), (256, 128), (256, 256), (192, 128), (96, 64), (160, 96)]
 
 
+_RESOURCES = {}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _instance_resources():
+    _RESOURCES.update(_listed_instances(resources=True))
+
+
 @pytest.mark.parametrize("bm,bn", SWEEP_BLOCKS, ids=lambda v: str(v))
 def test_no_plan_legal_configuration_lacks_a_kernel(bm, bn):
     """The plan either refuses a configuration (with a diagnostic) or binds
@@ -529,6 +551,10 @@ def test_no_plan_legal_configuration_lacks_a_kernel(bm, bn):
                         assert re.match(r"tb_plan_from_mlir: tb-[a-z0-9-]+: ", msg), msg
                         continue
                     bound += 1
+                    # register truth: the bound instance's compiled build holds
+                    # its wave tile in registers (no scratch)
+                    assert _RESOURCES[d.kernel_name][2] == 0, (d.kernel_name,
+                                                              _RESOURCES[d.kernel_name])
                     cfg = d.config
                     grid = configs.wave_grid(bm, bn, warps)
                     assert (cfg.wave_grid_m, cfg.wave_grid_n) == grid
@@ -548,3 +574,44 @@ def test_plan_over_operands_past_2gib():
     assert (cfg.m, cfg.n, cfg.k) == (262144, 32768, 8192)
     assert cfg.m * cfg.lda * 2 > 1 << 31 and cfg.m * cfg.ldc * 2 > 1 << 31
     assert cfg.k * cfg.ldb * 2 < 1 << 31
+
+
+def test_instance_resource_table_covers_every_instance():
+    """Every compiled instance has the compiler's register report in the
+    host-side table (generated at build time from hipcc's
+    kernel-resource-usage remarks): registers within a lone wave's 512, and
+    the known spilling builds read as spilling. The 32x32x16 builds of 128x128
+    wave tiles hold 256 accumulator registers and spill; the 16x16x32 loop
+    holds the same wave tile without scratch."""
+    res = _listed_instances(resources=True)
+    assert res and all(s >= 0 for _, _, s in res.values()), "instance without a report"
+    for name, (v, a, s) in res.items():
+        assert 0 < v <= 512 and 0 <= a <= 256 and v + a <= 512, (name, v, a)
+    assert res["tb_gemm_gfx950_128x128x64_w1x1_s2_out0"][2] > 0
+    assert res["tb_gemm_gfx950_256x128x32_w2x1_s2_out0"][2] > 0
+    assert res["tb_gemm_gfx950_128x128x64_w1x1_s2_out0_16x16x32"][2] == 0
+    assert res["tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"] [2] == 0
+    assert res["tb_gemm_gfx950_256x256x64_w2x2_s2_out0_16x16x32"][1] == 256
+
+
+def test_plan_refuses_an_instance_that_spills():
+    """Register truth: a configuration whose instance spills to scratch is
+    refused by the lowering with the compiler's figures (here 1 wave on a
+    128x128x64 block, forced onto 32x32x16), and by tb_desc_create; without
+    the forced instruction the plan binds the 16x16x32 build of the same
+    tile, which does not spill."""
+    forced = matmul_module(M=256, N=256, K=256, bm=128, bn=128, bk=64, warps=1,
+                           extra_op=', mma = "mfma_f32_32x32x16_f16"')
+    p = tb_opt(forced, f"--pass-pipeline={FULL}", check=False)
+    assert p.returncode == 1
+    assert re.search(r"tb-build-program-mapping-plan: gfx950 kernel instance "
+                     r"tb_gemm_gfx950_128x128x64_w1x1_s2_out0 spills \d+ bytes per lane "
+                     r"to scratch", p.stderr), p.stderr
+    with pytest.raises(tb.TbError, match="spills"):
+        tb.plan_from_mlir(forced)
+    d = tb.plan_from_mlir(forced.replace(', mma = "mfma_f32_32x32x16_f16"', ""))
+    assert d.kernel_name == "tb_gemm_gfx950_128x128x64_w1x1_s2_out0_16x16x32"
+    cfg = d.config
+    cfg.mfma = tb.MFMA_32X32X16
+    with pytest.raises(tb.TbError, match="spills"):
+        tb.GemmDesc.from_config(cfg)

@@ -12,13 +12,16 @@ Checks:
   (more tiles than programs), padded leading dimensions, ragged M, N and K
   (including a problem smaller than one wave tile, a K below one k-tile, and
   padding columns that must stay unwritten) and the fused steps;
-* bit-identity with the general loop at 8 waves (`w4x2`) and at 4 waves
-  (`w2x2`, 32x32x16): every output element is the same f32 sum of the same
-  products in the same k order (in 32x32x16 or 16x16x32 steps), and the
-  test pins that the two MFMA shapes round it alike;
+* bit-identity with the general loop (32x32x16, here on 4 waves of 64x64
+  over 128x128x64 blocks: the 32x32x16 builds of the same 256x256 block,
+  4 waves of 128x128 or 8 waves of 64x128 with the fused steps, spill and
+  are refused) and with the 16x16x32 loop's 128x128x64 build: every output
+  element is the same f32 sum of the same products in the same k order (in
+  32x32x16 or 16x16x32 steps), whatever the tiling, and the test pins that
+  the two MFMA shapes round it alike;
 * 40 seeded random ragged shapes (any M, N and K multiples of 8, every
   program order, padded leading dimensions) against the oracle and bit for
-  bit against the 4-wave general loop;
+  bit against the general loop;
 * every compile-time variant of the fused steps (activation x whether a
   clamp is set), against the oracle and bit-identical between the 16x16x32
   instance and the general loop's fused instance, and the fused instance in
@@ -36,15 +39,19 @@ pytestmark = pytest.mark.gpu
 RTOL = 1e-2
 
 
-def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0, mfma16=False):
-    wgm, wgn = (2, 2) if waves == 4 else (4, 2)
-    tm, tn = -(-M // 256), -(-N // 256)
+def _cfg(M, N, K, waves, mapping, programs=None, ld_pad=0, xcd=0, mfma16=False, block=256):
+    """The 4-wave 256x256x64 tile (block=256), or a 128x128x64 block on 4
+    waves of 64x64 (block=128: the general loop, or with mfma16 the 16x16x32
+    loop) for the bit-identity comparisons."""
+    assert waves == 4
+    tm, tn = -(-M // block), -(-N // block)
     return tb.GemmConfig(
         m=M, n=N, k=K, lda=K + ld_pad, ldb=N + ld_pad, ldc=N + ld_pad,
-        c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, block_m=256, block_n=256,
-        block_k=64, num_waves=waves, wave_grid_m=wgm, wave_grid_n=wgn, stages=2,
+        c_dtype=tb.DTYPE_F16, acc_init=tb.ACC_INIT_ZERO, block_m=block, block_n=block,
+        block_k=64, num_waves=waves, wave_grid_m=2, wave_grid_n=2, stages=2,
         mapping=mapping, group_m=8 if mapping != tb.MAP_TILE else 1, split_k=1,
-        reduction=tb.RED_NONE, num_programs=programs or tm * tn, xcd_remap=xcd,
+        reduction=tb.RED_NONE, num_programs=programs or tm * tn,
+        xcd_remap=xcd if (programs or tm * tn) % 8 == 0 else 0,
         mfma=tb.MFMA_16X16X32 if mfma16 else tb.MFMA_32X32X16)
 
 
@@ -101,26 +108,29 @@ def test_mfma16_matches_oracle_and_general_loop(M, N, K, mapping, programs, pad,
     bad, err, worst = oracle.check_tolerance(got16, ref, rtol=RTOL)
     print(f"  16x16x32: violations={bad} max|err|={err:.3e}", flush=True)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
-    for waves in (8, 4):
-        name, got = _run(_cfg(M, N, K, waves, mapping, programs, pad, xcd), A, B, device, pad)
-        assert "16x16x32" not in name
+    for mfma16 in (False, True):  # 128x128x64: the general loop, the 16x16x32 loop
+        name, got = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd, mfma16, block=128),
+                         A, B, device, pad)
+        assert name.startswith("tb_gemm_gfx950_128x128x64_w2x2_s2_out0")
+        assert ("16x16x32" in name) == mfma16
         assert np.array_equal(got16.view(np.uint16), got[:, :N].view(np.uint16)), name
 
 
 def test_mfma16_fused_steps(device):
     """Bias (f32), tanh GELU and a clamp on the 16x16x32 instance, against the
-    oracle's epilogue, and bit-identical to the 8-wave fused instance."""
+    oracle's epilogue, and bit-identical to the general loop's fused
+    instance (128x128x64 on 4 waves)."""
     M, N, K = 512, 768, 192
     print(f"wide fused {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0710, oracle.UNIFORM)
     bias = oracle.fill_f16(1, N, 0x5EED0711, oracle.UNIFORM, 1.0).reshape(N).astype(np.float32)
     outs = []
-    for waves in (4, 8):
-        cfg = _cfg(M, N, K, waves, tb.MAP_GROUPED_TILE, mfma16=waves == 4)
+    for block in (256, 128):
+        cfg = _cfg(M, N, K, 4, tb.MAP_GROUPED_TILE, mfma16=block == 256, block=block)
         cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F32, tb.ACT_GELU_TANH
         cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = tb.CLAMP_MIN | tb.CLAMP_MAX, -0.25, 3.0
         name, got = _run(cfg, A, B, device, bias=bias)
-        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
+        assert name.endswith("_16x16x32_epi" if block == 256 else "_out0_epi")
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), 2, 3, -0.25, 3.0)
@@ -140,19 +150,19 @@ EPI_VARIANTS = [(act, cl, -0.25, 0.5) for act in (0, 1, 2, 3) for cl in (0, 1, 3
                          ids=[f"act{v[0]}_clamp{v[1]}" for v in EPI_VARIANTS])
 def test_fused_step_variants(act, clamp, lo, hi, device):
     """Each activation with no clamp, a lower clamp and both clamps, on the
-    16x16x32 instance and on the general loop's fused 8-wave instance: both
-    match the oracle's epilogue and are bit-identical to each other."""
+    16x16x32 instance and on the general loop's fused 128x128x64 instance:
+    both match the oracle's epilogue and are bit-identical to each other."""
     M, N, K = 512, 512, 128
     print(f"wide fused variant act {act} clamp {clamp}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0720 + 4 * act + clamp, oracle.NORMAL)
     bias = oracle.fill_f16(1, N, 0x5EED0721, oracle.UNIFORM, 1.0).reshape(N)
     outs = []
-    for waves in (4, 8):
-        cfg = _cfg(M, N, K, waves, tb.MAP_GROUPED_TILE, mfma16=waves == 4)
+    for block in (256, 128):
+        cfg = _cfg(M, N, K, 4, tb.MAP_GROUPED_TILE, mfma16=block == 256, block=block)
         cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F16, act
         cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = clamp, lo, hi
         name, got = _run(cfg, A, B, device, bias=bias)
-        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
+        assert name.endswith("_16x16x32_epi" if block == 256 else "_out0_epi")
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), act, clamp, lo, hi)
@@ -165,20 +175,20 @@ def test_fused_step_variants(act, clamp, lo, hi, device):
 def test_fused_steps_persistent(device):
     """The fused 16x16x32 instance in persistent grouped order (9 tiles on 4
     programs, so a program runs its epilogue, then another tile's main
-    loop): against the oracle and bit-identical to the 8-wave fused
-    instance in plain grouped order."""
+    loop): against the oracle and bit-identical to the general loop's fused
+    128x128x64 instance in plain grouped order."""
     M, N, K = 768, 768, 192
     print(f"wide fused persistent {M}x{N}x{K}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0730, oracle.NORMAL)
     bias = oracle.fill_f16(1, N, 0x5EED0731, oracle.UNIFORM, 1.0).reshape(N).astype(np.float32)
     outs = []
-    for waves, mapping, programs in ((4, tb.MAP_PERSISTENT_GROUPED, 4),
-                                     (8, tb.MAP_GROUPED_TILE, None)):
-        cfg = _cfg(M, N, K, waves, mapping, programs, mfma16=waves == 4)
+    for block, mapping, programs in ((256, tb.MAP_PERSISTENT_GROUPED, 4),
+                                     (128, tb.MAP_GROUPED_TILE, None)):
+        cfg = _cfg(M, N, K, 4, mapping, programs, mfma16=block == 256, block=block)
         cfg.epi_bias, cfg.epi_activation = tb.EPI_BIAS_F32, tb.ACT_SILU
         cfg.epi_clamp, cfg.clamp_min, cfg.clamp_max = tb.CLAMP_MIN, -0.125, 0.0
         name, got = _run(cfg, A, B, device, bias=bias)
-        assert name.endswith("_16x16x32_epi" if waves == 4 else "_out0_epi")
+        assert name.endswith("_16x16x32_epi" if block == 256 else "_out0_epi")
         outs.append(got)
     ref = oracle.gemm_f64(A, B)
     oracle.epilogue_f64(ref, bias.astype(np.float64), 3, 1, -0.125, 0.0)
@@ -216,7 +226,7 @@ RANDOM_CASES = _random_cases(40, 0x5EED0780)
 def test_mfma16_random_shapes(M, N, K, mapping, programs, pad, xcd, device):
     """Random ragged shapes on the 16x16x32 instance (whole-K and partial-K
     builds): against the oracle, with padding columns untouched, and bit for
-    bit against the 4-wave general loop on the same shape."""
+    bit against the general loop (128x128x64 on 4 waves) on the same shape."""
     print(f"wide random {M}x{N}x{K} mapping {mapping} programs {programs} pad {pad} "
           f"xcd {xcd}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0781 + M + 3 * N + 7 * K, oracle.NORMAL)
@@ -228,6 +238,7 @@ def test_mfma16_random_shapes(M, N, K, mapping, programs, pad, xcd, device):
     got16 = got16[:, :N]
     bad, err, worst = oracle.check_tolerance(got16, oracle.gemm_f64(A, B), rtol=RTOL)
     assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
-    name, got = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd), A, B, device, pad)
+    name, got = _run(_cfg(M, N, K, 4, mapping, programs, pad, xcd, block=128), A, B, device,
+                     pad)
     assert "16x16x32" not in name
     assert np.array_equal(got16.view(np.uint16), got[:, :N].view(np.uint16)), name
