@@ -221,6 +221,16 @@ int tb_clock_probe(uint64_t *out, int32_t workgroups, int32_t window_ticks, void
 int tb_kernel_count(void);
 const char *tb_kernel_name(int i);
 
+/* The compiler's register report for kernel instance i (partial_k != 0: its
+ * build for a partial last k-tile, K % block_k != 0): VGPRs and AGPRs per
+ * wave and scratch bytes per lane, from the build-time table of hipcc's
+ * kernel-resource-usage remarks. The plan pipeline and tb_desc_create refuse
+ * an instance whose scratch is not zero. No counterpart in the reference:
+ * here every instance is compiled ahead of time, so its register use is
+ * known when the plan binds. */
+int tb_kernel_resources(int i, int32_t partial_k, int32_t *vgprs, int32_t *agprs,
+                        int32_t *scratch_bytes);
+
 /* The s_waitcnt depths compiled into kernel instance i: vmcnt at the
  * prologue's wait, vmcnt at the per-k-tile barrier, and lgkmcnt at that
  * barrier (-1: none, the compiler orders the LDS reads). The plan's AsyncPlan

@@ -140,6 +140,8 @@ def lib() -> ctypes.CDLL:
     L.tb_clock_probe.argtypes = [vp, i32, i32, vp]
     L.tb_clock_probe.restype = ctypes.c_int
     L.tb_kernel_count.restype = ctypes.c_int
+    L.tb_kernel_resources.argtypes = [i32, i32] + [ctypes.POINTER(ctypes.c_int32)] * 3
+    L.tb_kernel_resources.restype = ctypes.c_int
     L.tb_kernel_name.argtypes = [ctypes.c_int]
     L.tb_kernel_name.restype = ctypes.c_char_p
     _lib = L
@@ -379,3 +381,17 @@ def probe_clock_mhz(readings) -> float | None:
 def kernel_names() -> list[str]:
     L = lib()
     return [L.tb_kernel_name(i).decode() for i in range(L.tb_kernel_count())]
+
+
+def kernel_resources(partial_k: bool = False) -> dict[str, tuple[int, int, int]]:
+    """name -> (VGPRs, AGPRs, scratch bytes per lane) of every compiled
+    instance (partial_k: its build for a partial last k-tile), from the
+    compiler's report. The plan and tb_desc_create refuse an instance whose
+    scratch is not zero."""
+    L = lib()
+    out = {}
+    for i in range(L.tb_kernel_count()):
+        v = [ctypes.c_int32() for _ in range(3)]
+        _check(L.tb_kernel_resources(i, int(partial_k), *[ctypes.byref(x) for x in v]))
+        out[L.tb_kernel_name(i).decode()] = tuple(x.value for x in v)
+    return out

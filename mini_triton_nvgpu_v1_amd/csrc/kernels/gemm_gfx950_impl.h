@@ -129,6 +129,24 @@ __device__ __forceinline__ void static_for(F &&f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
+// The wait between the last inline-asm MFMA and the first read of the
+// accumulators. The compiler does not see the latency of an asm MFMA: it
+// places a read of a finished tile (the epilogue's, or a copy at a merge)
+// anywhere after that tile's last asm, even two instructions after it,
+// ahead of the MFMAs still running on the other tiles. Here 24 wait states
+// (three s_nop 7) are followed by an empty asm per tile that takes the tile
+// as an in-out AGPR operand: every later use reads that asm's result, so no
+// read can move above the waits.
+template <int TI, int TJ>
+__device__ __forceinline__ void acc_read_fence(f32x4 (&acc)[TI][TJ]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      asm volatile("" : "+a"(acc[i][j]));
+}
+
 // Runs block(i, act, clamp) for the epilogue's 16-row blocks i = 0 .. NB-1,
 // with EPI the activation and clamp of the launch dispatched once per block
 // (a block's code is specialised to them); without, the plain block.
@@ -625,8 +643,8 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
   kstep1(Q{}, E{}); // the last k-tile after its barrier point
   // Sched::ACC_READ_WAITS (24) wait states between the last MFMA and the
   // first accumulator read
-  static_assert(Sched::ACC_READ_WAITS == 24, "three s_nop 7 below");
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  static_assert(Sched::ACC_READ_WAITS == 24, "three s_nop 7 in the fence");
+  acc_read_fence(acc);
   wait_vmcnt<0>(); // the zero loads past the end have landed too
 
   // f16 C through LDS: each wave's 128x128 tile goes to its own 32 KiB,

@@ -78,7 +78,11 @@ struct Mfma16GTile {
   // ---- slot schedule ----------------------------------------------------
   // MFMA m of a k step: tile (m / TJ, m % TJ). Read op o of a k step: A0,
   // B0 (halves 0, 1), .., B(TJ-1), A1 .. A(TI-1): the order of first use.
-  static constexpr int BQ = NM >= 64 ? 8 : (NM >= 32 ? 4 : 2);
+  // the barrier sits before slot BQ of a k-tile's last k step; with 32-deep
+  // k-tiles at the k-tile's start (BQ = 0), so that a loop body is exactly
+  // one k-tile and the loop needs no tail whose fragment buffer depends on
+  // the k-tile count's parity
+  static constexpr int BQ = KS == 1 ? 0 : (NM >= 64 ? 8 : (NM >= 32 ? 4 : 2));
   static constexpr bool op_is_a(int o) { return o == 0 || o > 2 * TJ; }
   static constexpr int op_index(int o) {
     return o == 0 ? 0 : (o > 2 * TJ ? o - 2 * TJ : (o - 1) / 2);
@@ -323,7 +327,6 @@ __device__ __forceinline__ void mfma16g_tile(const GemmParams &p, int m0, int n0
     asm volatile("" ::: "memory");
   };
   using F = std::integral_constant<bool, false>;
-  using Tr = std::integral_constant<bool, true>;
   // buffer of k step ks of k-tile phase q (q = k-tile index mod U)
   auto buf_of = [](auto q_c, auto ks_c) {
     constexpr int Q = decltype(q_c)::value, KSI = decltype(ks_c)::value;
@@ -408,9 +411,9 @@ __device__ __forceinline__ void mfma16g_tile(const GemmParams &p, int m0, int n0
   wait_vmcnt<T::VM_PROLOGUE>();
   barrier();
   if constexpr (KS == 1) {
-    // 32-deep k-tiles: k-tile 0's only k step runs on both sides of its
-    // barrier, so its MFMAs cannot all be the first; the accumulators start
-    // from a zero product instead (srcC = 0, rule (a))
+    // 32-deep k-tiles: k-tile 0 runs in the loop's first body, whose code
+    // serves every k-tile; the accumulators start from a zero product
+    // instead (srcC = 0, rule (a))
     const half8 zf = {};
     auto zero = [&](int m) {
       asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %1, 0"
@@ -429,40 +432,36 @@ __device__ __forceinline__ void mfma16g_tile(const GemmParams &p, int m0, int n0
     using HI = std::integral_constant<int, KSI + 1 < KS ? NM : BQ>;
     kstep(Z{}, ks_c, Z{}, HI{}, std::integral_constant<bool, KSI == 0 && KS == 2>{}, nothing);
   });
+  // The loop: U bodies per trip, body q of a trip at phase q (k-tile it = 0
+  // mod U at the trip's start). With 64-deep k-tiles it leaves after the
+  // body of k-tile nk - 2, whichever body of the trip that is, and the tail
+  // runs the last k-tile after its barrier point (buffer 1 whatever the
+  // phase; no refill, no barrier). With 32-deep k-tiles a body is a whole
+  // k-tile and the loop leaves after the body of k-tile nk - 1, whose reads
+  // of k-tile nk land zeros and are not used: no tail, so no code path
+  // after the loop depends on the parity of nk (at such a merge the
+  // compiler would copy accumulators the last MFMAs are still writing: the
+  // asm hides their latency).
+  const int last_body = KS == 2 ? nk - 1 : nk;
   int it = 0;
-  // the loop: U bodies per trip, body q of a trip at phase q (k-tile it = 0
-  // mod U at the trip's start); it leaves after the body of k-tile nk - 2,
-  // whichever body of the trip that is
-  if (it < nk - 1) {
+  if (it < last_body) {
     for (;;) {
       bool done = false;
       static_for<U>([&](auto q_c) {
         if (!done) {
           body(it, q_c, F{});
           ++it;
-          done = it >= nk - 1;
+          done = it >= last_body;
         }
       });
       if (done)
         break;
     }
   }
-  // the last k-tile (nk - 1) after its barrier point: no refill, no barrier
-  auto tail = [&](auto q_c, auto first_c) {
-    kstep(q_c, LAST{}, QB{}, ENDS{}, first_c, nothing);
-  };
-  if constexpr (KS == 2) {
-    tail(Z{}, F{}); // buffer 1 whatever the phase
-  } else {
-    // 32-deep k-tiles: the last k-tile's buffer is its index's parity (its
-    // stage does not matter: no reads follow)
-    if ((nk - 1) & 1)
-      tail(std::integral_constant<int, 1>{}, F{});
-    else
-      tail(Z{}, F{});
-  }
+  if constexpr (KS == 2)
+    kstep(Z{}, LAST{}, QB{}, ENDS{}, F{}, nothing);
   // (b) 24 wait states between the last MFMA and the first accumulator read
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  acc_read_fence(acc);
   wait_vmcnt<0>(); // the zero loads past the end have landed too
 
   // ---- epilogue: 16-row blocks of the wave tile through this wave's LDS ----

@@ -459,4 +459,28 @@ int tb_kernel_waits(int i, int32_t *vm_prologue, int32_t *vm_loop, int32_t *lgkm
   return 0;
 }
 
+int tb_kernel_resources(int i, int32_t partial_k, int32_t *vgprs, int32_t *agprs,
+                        int32_t *scratch_bytes) {
+  const tbk::KernelEntry *e = tbk::kernel_at(i);
+  if (!e || !vgprs || !agprs || !scratch_bytes)
+    return fail("tb_kernel_resources: no instance " + std::to_string(i) + " or NULL output");
+  tb::InstanceKey ik;
+  ik.bm = e->key.bm;
+  ik.bn = e->key.bn;
+  ik.bk = e->key.bk;
+  ik.wgm = e->key.wgm;
+  ik.wgn = e->key.wgn;
+  ik.out = e->key.out;
+  ik.stages = e->key.stages;
+  ik.epi = e->key.epi;
+  ik.mfma = e->key.mfma;
+  const tb::InstanceResources r = tb::instanceResources(ik, partial_k != 0);
+  if (!r.known)
+    return fail(std::string("tb_kernel_resources: no compiler report for ") + e->name);
+  *vgprs = (int32_t)r.vgprs;
+  *agprs = (int32_t)r.agprs;
+  *scratch_bytes = (int32_t)r.scratchBytes;
+  return 0;
+}
+
 } // extern "C"

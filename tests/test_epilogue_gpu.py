@@ -77,8 +77,8 @@ F16_CASES = [
        clamp_min=-0.5, clamp_max=2.0),
     _w(configs.RAGGED_128, "tile128_bias16_silu_max", bias="f16", activation="silu",
        clamp_max=0.75),
-    _w(configs.ROOFLINE, "w4x2_512_bias32_gelu", M=512, N=512, K=256, bias="f32",
-       activation="gelu_tanh", num_waves=8),
+    _w(configs.ROOFLINE, "w4x2_512x256_bias32_gelu", M=512, N=512, K=256, bias="f32",
+       activation="gelu_tanh", block=(256, 128, 64), num_waves=8),
     _w(configs.ROOFLINE, "w2x2_512_bias16_silu", M=512, N=768, K=192, bias="f16",
        activation="silu", clamp_min=-0.5),
     _w(configs.RAGGED, "ragged_clamp_only", clamp_min=-0.25),
@@ -106,7 +106,7 @@ def test_fused_epilogue_f32_accumulate(device):
     print(f"case {w.name}", flush=True)
     desc = tb.plan_from_mlir(text)
     assert desc.config.acc_init == tb.ACC_INIT_LOAD_C
-    assert desc.kernel_name.endswith("_out2_epi")
+    assert "_out2" in desc.kernel_name and desc.kernel_name.endswith("_epi")
     A, B = oracle.config_inputs(w.M, w.N, w.K, w.seed, w.dist)
     C0 = oracle.fill_f16(w.M, w.N, 0x5EED0601, oracle.UNIFORM, 2.0).astype(np.float32)
     _run_and_check(desc, w, A, B, device, c0=C0, c_dtype=torch.float32)

@@ -195,10 +195,14 @@ RAGGED_SHAPES = [(1, 8, 8), (33, 24, 16), (97, 88, 40), (200, 136, 72),
 
 
 @pytest.mark.parametrize("M,N,K", RAGGED_SHAPES)
-@pytest.mark.parametrize("tile", [(64, 64, 32, 2, 2), (128, 128, 64, 2, 2),
-                                  (256, 256, 64, 2, 2)])
+# (block, wave grid, 16x16x32): the 256x256 tile on four waves holds its
+# 128x128 wave tiles in registers only on 16x16x32 (its 32x32x16 build spills
+# and is refused)
+@pytest.mark.parametrize("tile", [(64, 64, 32, 2, 2, 0), (128, 128, 64, 2, 2, 0),
+                                  (128, 128, 64, 2, 2, 1), (128, 128, 32, 2, 2, 1),
+                                  (256, 256, 64, 2, 2, 1)])
 def test_ragged_edges(M, N, K, tile, device):
-    bm, bn, bk, wgm, wgn = tile
+    bm, bn, bk, wgm, wgn, mfma16 = tile
     print(f"ragged {M}x{N}x{K} tile {tile}", flush=True)
     A, B = oracle.config_inputs(M, N, K, 0x5EED0100 + M, oracle.UNIFORM)
     tm, tn = -(-M // bm), -(-N // bn)
@@ -208,7 +212,7 @@ def test_ragged_edges(M, N, K, tile, device):
                         block_k=bk, num_waves=wgm * wgn, wave_grid_m=wgm,
                         wave_grid_n=wgn, stages=2, mapping=mapping, group_m=8,
                         split_k=1, reduction=tb.RED_NONE, num_programs=tm * tn,
-                        xcd_remap=8)
+                        xcd_remap=8, mfma=tb.MFMA_16X16X32 if mfma16 else tb.MFMA_32X32X16)
     got = run_desc(tb.GemmDesc.from_config(cfg), A, B, device)
     check(got, A, B)
 
@@ -228,6 +232,20 @@ def _every_instance():
         seen.add((bm, bn, bk, wgm, wgn, int(stages[1:]), int(out[3:]), int(epi),
                   int(mfma16)))
     return sorted(seen)
+
+
+_RESOURCES = {}
+
+
+def _spills(inst, partial_k: bool) -> bool:
+    """The instance's build (for a partial last k-tile when partial_k) uses
+    scratch, in the compiler's report the library carries."""
+    bm, bn, bk, wgm, wgn, stages, out, epi, mfma16 = inst
+    if partial_k not in _RESOURCES:
+        _RESOURCES[partial_k] = tb.kernel_resources(partial_k=partial_k)
+    name = (f"tb_gemm_gfx950_{bm}x{bn}x{bk}_w{wgm}x{wgn}_s{stages}_out{out}"
+            f"{'_16x16x32' if mfma16 else ''}{'_epi' if epi else ''}")
+    return _RESOURCES[partial_k][name][2] > 0
 
 
 # fused steps per output mode of the `_epi` instances: (bias kind, activation,
@@ -282,14 +300,21 @@ def test_every_instance(inst, device):
                             mapping=tb.MAP_SPLIT_K, split_k=2,
                             reduction=tb.RED_ATOMIC, num_programs=tm * tn * 2, **kw)
         c_dtype = torch.float32
+    if epi:
+        kind, act, bits, lo, hi = EPI_STEPS[out]
+        cfg.epi_bias, cfg.epi_activation, cfg.epi_clamp = kind, act, bits
+        cfg.clamp_min, cfg.clamp_max = lo, hi
+    if _spills(inst, partial_k=K % bk != 0):
+        # register truth: a build that spills to scratch is refused, with the
+        # compiler's figures, and never launched
+        with pytest.raises(tb.TbError, match="spills .* bytes per lane to scratch"):
+            tb.GemmDesc.from_config(cfg)
+        return
     if not epi:
         desc = tb.GemmDesc.from_config(cfg)
         got = run_desc(desc, A, B, device, c_init=init, c_dtype=c_dtype)
         check(got, A, B, init=init)
         return
-    kind, act, bits, lo, hi = EPI_STEPS[out]
-    cfg.epi_bias, cfg.epi_activation, cfg.epi_clamp = kind, act, bits
-    cfg.clamp_min, cfg.clamp_max = lo, hi
     desc = tb.GemmDesc.from_config(cfg)
     assert desc.kernel_name.endswith(f"_out{out}{'_16x16x32' if mfma16 else ''}_epi")
     bias = oracle.fill_f16(1, N, 0x5EED0300 + N, oracle.UNIFORM, 1.0).reshape(N)

@@ -18,7 +18,7 @@ import torch
 
 import mini_triton_nvgpu_v1_amd as tb
 import oracle
-from test_gemm_gpu import _every_instance, run_desc
+from test_gemm_gpu import _every_instance, _spills, run_desc
 
 pytestmark = pytest.mark.gpu
 RTOL = 1e-2
@@ -65,7 +65,10 @@ def _case(rng, insts, case):
 
 
 def test_random_parity(device):
-    insts = [i for i in _every_instance() if not i[7]]  # plain (unfused) instances
+    # plain (unfused) instances; those whose builds spill are refused (register
+    # truth) and have their own test
+    insts = [i for i in _every_instance()
+             if not i[7] and not _spills(i, False) and not _spills(i, True)]
     rng = random.Random(0x5EED0900)
     failures = []
     for case in range(CASES):
@@ -129,7 +132,8 @@ def _fused_case(rng, insts, case):
 
 
 def test_random_fused_parity(device):
-    insts = [i for i in _every_instance() if i[7]]  # `_epi` instances
+    insts = [i for i in _every_instance()  # `_epi` instances that hold their tile
+             if i[7] and not _spills(i, False) and not _spills(i, True)]
     rng = random.Random(0x5EED0A00)
     failures = []
     for case in range(FUSED_CASES):
