@@ -34,7 +34,7 @@ PEAK_TFLOPS_F16 = 2500.0  # MI355X dense FP16 MFMA (published, no sparsity)
 PEAK_HBM_GBS = 8000.0
 PEAK_CLOCK_MHZ = 2400.0  # the clock the dense peak is quoted at (1024 SIMDs x 1024 FLOP/clk)
 XCDS = 8  # MI355X: 8 XCDs of 32 CUs
-PROBE_TICKS = 2000  # clock-probe window: 20 us of the 100 MHz counter
+STAMP_WGS = 1024  # one-wave clock stamps per reading: about every CU is stamped
 
 
 def log(msg: str) -> None:
@@ -93,22 +93,28 @@ def time_workload(w, steps: int, warmup: int, device, rounds: int = 5,
     for _ in range(warmup):
         launch()
     walls, events, clocks = [], [], []
-    # a shader-clock probe (one wave per XCD, 20 us) on the launch stream right
-    # after each round's timed region: the clock the round's kernels ran at
-    probes = torch.zeros((rounds, 3 * XCDS), dtype=torch.int64, device=device)
+    # shader-clock stamps (1024 one-wave workgroups) on the launch stream
+    # right before and right after each round's launches: per CU stamped
+    # both times, the cycles between its two stamps over the 100 MHz ticks
+    # between them is the mean clock the round's kernels ran at (the stamps
+    # add a few us to a round of tens of ms); the median over CUs
+    stamps = torch.zeros((rounds, 2, 3 * STAMP_WGS), dtype=torch.int64, device=device)
     for r in range(rounds):
         region = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         torch.cuda.synchronize(device)
         t0 = time.perf_counter()
+        tb.clock_stamp(stamps[r, 0], STAMP_WGS, stream=stream)
         region[0].record(stream)
         for _ in range(steps):
             launch()
         region[1].record(stream)
-        tb.clock_probe(probes[r], XCDS, PROBE_TICKS, stream=stream)
+        tb.clock_stamp(stamps[r, 1], STAMP_WGS, stream=stream)
         torch.cuda.synchronize(device)
         walls.append(time.perf_counter() - t0)
         events.append(region[0].elapsed_time(region[1]) / steps)
-    clocks = [tb.probe_clock_mhz(p) for p in probes.tolist()]
+    for before, after in stamps.tolist():
+        per_cu = tb.stamps_clock_mhz(before, after)
+        clocks.append(statistics.median(per_cu.values()) if per_cu else None)
     if C0 is not None:
         # the timed launches accumulated into C: check one more launch on the
         # prior C instead
@@ -151,17 +157,20 @@ def verify_output(w, A, B, C, bias, C0=None):
 
 
 def clock_summary(r) -> dict:
-    """The shader clock of the timed rounds (a probe on the launch stream
-    right after each round, mean over the 8 XCDs), the median round's value.
-    The caller adds the fraction of peak the kernel reaches per clock cycle:
-    the achieved rate over the peak scaled from 2.4 GHz to that clock."""
+    """The shader clock the timed rounds ran at (per round: stamps on the
+    launch stream right before and right after its launches, the cycles
+    between them over the 100 MHz ticks between them, mean over the XCDs),
+    the median round's value. The caller adds the fraction of peak the kernel
+    reaches per clock cycle: the achieved rate over the peak scaled from
+    2.4 GHz to that clock."""
     clk = [c for c in r["round_clock_mhz"] if c]
     if not clk:
         return {"mhz": None}
     mhz = statistics.median(clk)
     return {"mhz": round(mhz, 1), "round_mhz": [round(c, 1) for c in clk],
-            "source": "s_memtime / s_memrealtime over a 20 us window, one wave per XCD, "
-                      "launched on the stream right after each timed round",
+            "source": "s_memtime / s_memrealtime stamps (1024 one-wave workgroups) on the "
+                      "launch stream right before and right after each timed round's "
+                      "launches, paired per CU, median over CUs",
             "peak_clock_mhz": PEAK_CLOCK_MHZ}
 
 

@@ -217,6 +217,17 @@ int tb_fill_seeded_f16(void *dst, int64_t rows, int64_t cols, int64_t ld,
  * it reads the clock that work ran at. `out` is a device pointer. */
 int tb_clock_probe(uint64_t *out, int32_t workgroups, int32_t window_ticks, void *stream);
 
+/* Harness helper (no reference counterpart). Launches `workgroups` one-wave
+ * workgroups on `stream`; each writes three uint64 to out[3w..3w+2]: where
+ * it ran (XCC id << 8 | the SE, SH and CU fields of HW_ID) and the current
+ * counts of its CU's shader clock (s_memtime) and of the 100 MHz real-time
+ * counter (s_memrealtime). Both counters run on while other kernels execute,
+ * so a stamp before and a stamp after some work on the same stream give, for
+ * each CU both reached, the mean shader clock over that work: (cycles after
+ * - cycles before) / (ticks after - ticks before) * 100 MHz. `out` is a
+ * device pointer. */
+int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream);
+
 /* Number of compiled kernel instances and the name of instance i. */
 int tb_kernel_count(void);
 const char *tb_kernel_name(int i);

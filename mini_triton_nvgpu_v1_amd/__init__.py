@@ -139,6 +139,8 @@ def lib() -> ctypes.CDLL:
     L.tb_fill_seeded_f16.restype = ctypes.c_int
     L.tb_clock_probe.argtypes = [vp, i32, i32, vp]
     L.tb_clock_probe.restype = ctypes.c_int
+    L.tb_clock_stamp.argtypes = [vp, i32, vp]
+    L.tb_clock_stamp.restype = ctypes.c_int
     L.tb_kernel_count.restype = ctypes.c_int
     L.tb_kernel_resources.argtypes = [i32, i32] + [ctypes.POINTER(ctypes.c_int32)] * 3
     L.tb_kernel_resources.restype = ctypes.c_int
@@ -376,6 +378,34 @@ def probe_clock_mhz(readings) -> float | None:
     cyc = sum(int(readings[3 * i + 1]) for i in range(len(readings) // 3))
     ticks = sum(int(readings[3 * i + 2]) for i in range(len(readings) // 3))
     return cyc / ticks * 100.0 if ticks > 0 else None
+
+
+def clock_stamp(out, workgroups: int = 1024, stream=None) -> None:
+    """Stamp (where, shader-clock count, 100 MHz count) from `workgroups`
+    one-wave workgroups into the 64-bit device tensor `out`, on `stream`;
+    `where` is XCC id << 8 | the SE, SH and CU fields of HW_ID."""
+    _check(lib().tb_clock_stamp(_ptr(out), workgroups, _stream_handle(stream)))
+
+
+def stamps_clock_mhz(before, after) -> dict:
+    """Per-CU mean shader clock between two clock_stamp readings (host lists
+    of (where, cycles, ticks) triples): for each CU present in both, (cycles
+    after - cycles before) / (ticks after - ticks before) * 100 MHz. A CU's
+    counter is its own, so only stamps of the same CU are paired (the first
+    reading of each CU in each stamp); pairs whose counters did not advance
+    are left out."""
+    def by_cu(r):
+        d = {}
+        for i in range(len(r) // 3):
+            d.setdefault(int(r[3 * i]), (int(r[3 * i + 1]), int(r[3 * i + 2])))
+        return d
+    b, a = by_cu(before), by_cu(after)
+    out = {}
+    for x in sorted(set(b) & set(a)):
+        dc, dt = a[x][0] - b[x][0], a[x][1] - b[x][1]
+        if dc > 0 and dt > 0:
+            out[x] = dc / dt * 100.0
+    return out
 
 
 def kernel_names() -> list[str]:

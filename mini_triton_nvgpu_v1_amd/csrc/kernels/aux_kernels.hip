@@ -174,6 +174,28 @@ __global__ __launch_bounds__(64) void clock_probe_kernel(unsigned long long *out
   }
 }
 
+// One reading per workgroup, no window: (where, shader-clock count, 100 MHz
+// count), `where` = XCC id << 8 | the SE, SH and CU fields of HW_ID (bits
+// 8..15). The shader-clock counter is not common to the CUs of an XCD, so
+// two stamps on a stream around some work give the mean clock over that work
+// per CU that both stamps reached: cycles between them / ticks between them.
+__global__ __launch_bounds__(64) void clock_stamp_kernel(unsigned long long *out) {
+  unsigned xcc, hwid;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(xcc));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID, 8, 8)" : "=s"(hwid));
+  const unsigned long long t = read_shader_clock(), r = read_real_clock();
+  if (threadIdx.x == 0) {
+    out[3 * blockIdx.x + 0] = ((xcc & 0xfu) << 8) | (hwid & 0xffu);
+    out[3 * blockIdx.x + 1] = t;
+    out[3 * blockIdx.x + 2] = r;
+  }
+}
+
+hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s) {
+  hipLaunchKernelGGL(clock_stamp_kernel, dim3(workgroups), dim3(64), 0, s, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_clock_probe(unsigned long long *out, int workgroups, unsigned window,
                               hipStream_t s) {
   hipLaunchKernelGGL(clock_probe_kernel, dim3(workgroups), dim3(64), 0, s, out, window);

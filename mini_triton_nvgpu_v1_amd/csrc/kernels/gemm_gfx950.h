@@ -234,5 +234,7 @@ hipError_t launch_fill(void *dst, int64_t rows, int64_t cols, int64_t ld,
 // ticks) over a window of `window` ticks.
 hipError_t launch_clock_probe(unsigned long long *out, int workgroups, unsigned window,
                               hipStream_t s);
+// `workgroups` one-wave stamps of (XCC id, shader-clock count, 100 MHz count).
+hipError_t launch_clock_stamp(unsigned long long *out, int workgroups, hipStream_t s);
 
 } // namespace tbk

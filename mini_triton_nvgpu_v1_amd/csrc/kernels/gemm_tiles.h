@@ -173,7 +173,7 @@
 // with 32-deep k-tiles the fragment buffer of the last k-tile depends on
 // the k-tile count's parity, and with 192-256 accumulator registers held
 // the compiler spills at the two tails' merge.
-#define TBK_M16_SHAPES(S) S(128x128) S(256x128) S(128x256) S(256x64) S(192x128)
+#define TBK_M16_SHAPES(S) S(128x128) S(256x128) S(128x256) S(256x64) S(192x128) S(256x256)
 
 #define TBK_M16_TILES_128x128(X) \
   X(128, 128, 64, 2, 2, 2), X(128, 128, 64, 2, 2, 3), X(128, 128, 64, 2, 2, 4), \
@@ -194,6 +194,11 @@
 
 
 #define TBK_M16_TILES_256x64(X) X(256, 64, 64, 1, 1, 2)
+
+// 4 waves of 128x128 on 256x256 with 32-deep k-tiles in 3 or 4 LDS stages
+// (the same 128 KiB ring as the hand-scheduled 64-deep 2-stage tile, cut
+// into k-tiles of half the depth: half the loads and reads per barrier)
+#define TBK_M16_TILES_256x256(X) X(256, 256, 32, 2, 2, 3), X(256, 256, 32, 2, 2, 4)
 
 #define TBK_M16_TILES_192x128(X) \
   X(192, 128, 64, 2, 1, 2), X(192, 128, 64, 2, 1, 3), X(192, 128, 64, 2, 1, 4), \

@@ -442,6 +442,16 @@ int tb_clock_probe(uint64_t *out, int32_t workgroups, int32_t window_ticks, void
                    "hipLaunchKernel(clock probe)");
 }
 
+int tb_clock_stamp(uint64_t *out, int32_t workgroups, void *stream) {
+  if (!out || workgroups < 1 || workgroups > 1024)
+    return fail("tb_clock_stamp: out must be a device pointer and workgroups in 1..1024");
+  if (reinterpret_cast<uintptr_t>(out) % 8)
+    return fail("tb_clock_stamp: out must be 8-byte aligned");
+  return check_hip(tbk::launch_clock_stamp(reinterpret_cast<unsigned long long *>(out),
+                                           workgroups, reinterpret_cast<hipStream_t>(stream)),
+                   "hipLaunchKernel(clock stamp)");
+}
+
 int tb_kernel_count(void) { return tbk::kernel_count(); }
 
 const char *tb_kernel_name(int i) {
