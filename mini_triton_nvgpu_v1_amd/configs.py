@@ -240,4 +240,9 @@ FUSED = [dataclasses.replace(ROOFLINE, name="gemm_4096_bias_gelu", bias="f16",
 # prior C read, the sum written back as f32).
 F32_ACCUMULATE = [dataclasses.replace(ROOFLINE, name="gemm_4096_f32_accumulate",
                                       c_f32=True)]
-BY_NAME = {w.name: w for w in ALL + FUSED + F32_ACCUMULATE}
+# Profiling rows (not bench lines): the 16x16x32 loop's 4-wave 128x128 tile at
+# 2048^3 (1024 tiles, four per CU), against the hand-scheduled 256x256 tile's
+# MFMA-busy fraction at 4096^3.
+PROFILE_ROWS = [Workload("gemm_2048_tile128", 2048, 2048, 2048, 0x5EED0007, NORMAL,
+                         (128, 128, 64), num_waves=4, stages=3, group_m=8)]
+BY_NAME = {w.name: w for w in ALL + FUSED + F32_ACCUMULATE + PROFILE_ROWS}

@@ -227,6 +227,14 @@ __device__ __forceinline__ void map_program(const GemmParams &p, int pid,
   part = 0;
 }
 
+constexpr int cgcd_(int a, int b) { return b == 0 ? a : cgcd_(b, a % b); }
+// XOR phases over `units` swizzle units per row: the largest power of two
+// dividing `units` (so a unit XOR-ed with the phase stays inside its row),
+// at most `cap`
+constexpr int swizzle_phases(int units, int cap) {
+  return (units & -units) < cap ? (units & -units) : cap;
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int STAGES, int SPREAD_REQ = -1>
 struct GemmTile {
   static constexpr int NW = WGM * WGN; // waves
@@ -247,18 +255,32 @@ struct GemmTile {
   // B: 64-byte segments (the 32 columns two 16-lane tr groups read per row),
   // PP = rows per 256 B, MAXPH = min(4, segments per row); in 16-byte chunks
   // the XOR value is 4 * phase.
-  static constexpr int B_PP = 256 / (BN * 2) >= 1 ? 256 / (BN * 2) : 1;
-  static constexpr int B_MAXPH = BNC / 4 < 4 ? BNC / 4 : 4;
+  // PP: rows before a row's bank offset repeats, 256 / gcd(row bytes, 256)
+  // (2 for 384-byte rows, whose consecutive rows sit 128 bytes apart in the
+  // banks); MAXPH: at most 4, and a power of two dividing the segments per
+  // row, so the XOR keeps a chunk inside its row (2 for 6 segments)
+  static constexpr int B_PP = 256 / cgcd_(BN * 2, 256);
+  static constexpr int B_MAXPH = swizzle_phases(BNC / 4, 4);
   static constexpr int A_STAGE = BM * KCH;  // 16-byte chunks
   static constexpr int B_STAGE = BK * BNC;
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LDS_BYTES = STAGES * STAGE * 16;
-  // direct loads per thread per k-tile
-  static constexpr int LA = A_STAGE / NT;
-  static constexpr int LB = B_STAGE / NT;
+  // direct loads per thread per k-tile: whole load rounds of NT chunks; an
+  // operand stage of fewer chunks than the rounds cover (8 waves on a
+  // 32-deep k-tile of a 64- or 128-wide block) leaves whole waves idle in its
+  // last round: those waves issue their load anyway, from kOob (zeros) into a
+  // 1 KiB scratch row past the ring that nothing reads, so every wave issues
+  // the same loads and one vmcnt depth serves them all
+  static constexpr int LA = (A_STAGE + NT - 1) / NT;
+  static constexpr int LB = (B_STAGE + NT - 1) / NT;
   static constexpr int LPT = LA + LB;
+  static constexpr bool IDLE_ROUNDS = LA * NT != A_STAGE || LB * NT != B_STAGE;
+  static constexpr int SCRATCH_CHUNKS = IDLE_ROUNDS ? 64 : 0; // 1 KiB
+  static constexpr int LDS_BYTES = (STAGES * STAGE + SCRATCH_CHUNKS) * 16;
   static constexpr int A_ROWS_PER_LOAD = NT / KCH; // rows one load round covers
   static constexpr int B_ROWS_PER_LOAD = NT / BNC;
+  // B rows of 24 chunks (192 columns): a load round ends inside a row, so a
+  // lane's row and chunk differ per round and each round has its own offset
+  static constexpr bool B_RAGGED_ROUNDS = NT % BNC != 0;
 
   // ---- slot schedule (tiles with >= 4 MFMAs per k step) ------------------
   // A k-tile is NSLOT MFMA slots (KSTEPS x NMFMA). The one barrier per
@@ -325,12 +347,12 @@ struct GemmTile {
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
-  static_assert(BNC >= 8 && 64 % BNC == 0, "B rows of 64..512 halves");
-  static_assert(B_ROWS_PER_LOAD % B_PP == 0 &&
-                    (B_ROWS_PER_LOAD / B_PP) % B_MAXPH == 0,
+  static_assert(BNC >= 8 && (64 % BNC == 0 || BNC == 24), "B rows of 64..512 halves or 192");
+  static_assert(B_RAGGED_ROUNDS || LB == 1 ||
+                    (B_ROWS_PER_LOAD % B_PP == 0 && (B_ROWS_PER_LOAD / B_PP) % B_MAXPH == 0),
                 "a lane's B swizzle phase is the same in every load round");
-  static_assert(LA >= 1 && LA * NT == A_STAGE, "A loads per thread");
-  static_assert(LB >= 1 && LB * NT == B_STAGE, "B loads per thread");
+  static_assert(A_STAGE % 64 == 0 && B_STAGE % 64 == 0,
+                "an operand stage is whole waves' load rounds (idle lanes are whole waves)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KiB per workgroup");
   static_assert(VM_LOOP < 64 && VM_PROLOGUE < 64, "vmcnt range");
@@ -815,7 +837,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
   using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES, SPREAD_REQ>;
   constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
                 KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LPT = T::LPT;
-  __shared__ u32x4 lds[STAGES * T::STAGE];
+  __shared__ u32x4 lds[STAGES * T::STAGE + T::SCRATCH_CHUNKS];
   auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };
 
   const int tid = threadIdx.x;
@@ -844,10 +866,16 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     return a_pc ^ (((a_row0 + i * T::A_ROWS_PER_LOAD) / T::A_PP) % KCH);
   };
   // B: chunk q -> k row q / BNC, physical chunk q % BNC holding logical n
-  //    chunk (q % BNC) ^ (4 * ((row / B_PP) % B_MAXPH)), fixed per lane.
+  //    chunk (q % BNC) ^ (4 * ((row / B_PP) % B_MAXPH)), fixed per lane when
+  //    a round covers whole rows; else per round (B_RAGGED_ROUNDS)
   const int b_row0 = (wave * 64 + lane) / BNC;
-  const int b_pc = lane % BNC;
+  const int b_pc = (wave * 64 + lane) % BNC;
   const int b_lc = b_pc ^ (4 * ((b_row0 / T::B_PP) % T::B_MAXPH));
+  auto b_round_row = [&](int i) { return (i * T::NT + wave * 64 + lane) / BNC; };
+  auto b_round_lc = [&](int i) {
+    const int q = i * T::NT + wave * 64 + lane;
+    return (q % BNC) ^ (4 * (((q / BNC) / T::B_PP) % T::B_MAXPH));
+  };
 
   // ---- fragment-read geometry --------------------------------------------
   const int fr_a = wm * T::WTM + (lane & 31); // A rows of this lane's srcB
@@ -873,21 +901,15 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     const int kt_end = kt0 + nk;
 
     f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = (f32x16){};
-
     // C += A*B on small wave tiles of 4-wave workgroups (512 registers per
-    // lane): the prior C is loaded before the tile's first A/B loads, so its
-    // latency overlaps the main loop instead of following it. Issued first,
-    // these loads are older than every A/B load, so the main loop's vmcnt
-    // waits stay as they are.
-    constexpr bool PREFETCH_C = OUT == kOutF32Accum && !T::STAGED_F32_EPILOGUE &&
-                                TM * TN <= 4 && NW <= 4;
-    f32x4 c_pre[PREFETCH_C ? TM : 1][PREFETCH_C ? TN : 1][4];
-    if constexpr (PREFETCH_C) {
+    // lane): the prior C is the accumulators' starting value, as in the
+    // reference (LowerPipelineToNVGPU.cpp:2246-2263, C loaded into the
+    // accumulators before the K loop; the sum is C + a0 b0 + a1 b1 + ... in
+    // k order). Its loads are issued before the tile's first A/B loads, so
+    // their latency runs beside those loads, and the first MFMA (which waits
+    // for k-tile 0) finds them landed.
+    constexpr bool PRIOR_C_START = OUT == kOutF32Accum && TM * TN <= 4 && NW <= 4;
+    if constexpr (PRIOR_C_START) {
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
       const int row0 = m0 + wm * T::WTM + (lane & 31);
@@ -903,9 +925,18 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                 (row < p.M && col < p.N)
                     ? ((uint32_t)(row - m0) * (uint32_t)p.ldc + (uint32_t)col) * 4u
                     : kOob;
-            c_pre[i][j][g] = __builtin_bit_cast(
+            const f32x4 c = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[i][j][4 * g + r] = c[r];
           }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = (f32x16){};
     }
 
     // The k-dependent part of each global address is wave-uniform and rides
@@ -918,9 +949,28 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                                 ? ((uint32_t)b_row0 * (uint32_t)p.ldb +
                                    (uint32_t)(n0 + b_lc * 8)) * 2u
                                 : kOob;
+    // ragged B rounds: per round the lane's k row and its vector offset
+    // (column past N: kOob)
+    int b_rrow[T::B_RAGGED_ROUNDS ? T::LB : 1];
+    uint32_t b_rvoff[T::B_RAGGED_ROUNDS ? T::LB : 1];
+    if constexpr (T::B_RAGGED_ROUNDS) {
+#pragma unroll
+      for (int i = 0; i < T::LB; ++i) {
+        const int row = b_round_row(i), lc = b_round_lc(i);
+        b_rrow[i] = row;
+        b_rvoff[i] = (n0 + lc * 8) < p.N
+                         ? ((uint32_t)row * (uint32_t)p.ldb + (uint32_t)(n0 + lc * 8)) * 2u
+                         : kOob;
+      }
+    }
 
     // Direct load l (0 .. LPT-1) of k-tile kt into LDS stage `stage`:
     // A load rounds first (l < LA), then B rounds.
+    // the scratch row of the idle lanes of a last load round (past the ring),
+    // from the array's LDS address (the cast of an offset pointer instead
+    // makes the compiler emit an illegal null check against the aperture)
+    const uint32_t idle_lds =
+        (uint32_t)(uintptr_t)(TBK_LDS void *)lds + STAGES * T::STAGE * 16u;
     auto issue_load = [&](int kt, int stage, int l) {
       const int k0 = kt * BK;
       const bool kt_ok = kt < kt_end;
@@ -930,18 +980,31 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       if (l < LA) {
         const int i = l;
         const int lc = a_lchunk(i);
-        const bool ok = kt_ok && (k0 + lc * 8) < p.K && i * T::A_ROWS_PER_LOAD < a_rows_left;
-        load_lds16(ra4, a_lds + i * NW * 1024u, ok ? a_vrow + lc * 16u : kOob,
+        // wave-uniform: the round's chunks of this wave lie inside the stage
+        const bool live = (i * NW + wave) * 64 < T::A_STAGE;
+        const bool ok = live && kt_ok && (k0 + lc * 8) < p.K &&
+                        i * T::A_ROWS_PER_LOAD < a_rows_left;
+        load_lds16(ra4, live ? a_lds + i * NW * 1024u : idle_lds,
+                   ok ? a_vrow + lc * 16u : kOob,
                    k0 * 2 + i * T::A_ROWS_PER_LOAD * p.lda * 2);
       } else {
         const int i = l - LA;
         const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
-        const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
-        // unsigned: a lookahead k-tile past the end (voffset kOob) may put
-        // k0 past K, where the signed product could pass INT_MAX
-        load_lds16(rb4, b_lds + i * NW * 1024u,
-                   (kt_ok && krow < p.K) ? b_voff : kOob,
-                   (uint32_t)(k0 + i * T::B_ROWS_PER_LOAD) * (uint32_t)p.ldb * 2u);
+        const bool live = (i * NW + wave) * 64 < T::B_STAGE;
+        if constexpr (T::B_RAGGED_ROUNDS) {
+          // the round's rows ride in the vector offset; the k-tile's in the
+          // scalar one (unsigned: see below)
+          load_lds16(rb4, live ? b_lds + i * NW * 1024u : idle_lds,
+                     (live && kt_ok && k0 + b_rrow[i] < p.K) ? b_rvoff[i] : kOob,
+                     (uint32_t)k0 * (uint32_t)p.ldb * 2u);
+        } else {
+          const int krow = k0 + b_row0 + i * T::B_ROWS_PER_LOAD;
+          // unsigned: a lookahead k-tile past the end (voffset kOob) may put
+          // k0 past K, where the signed product could pass INT_MAX
+          load_lds16(rb4, live ? b_lds + i * NW * 1024u : idle_lds,
+                     (live && kt_ok && krow < p.K) ? b_voff : kOob,
+                     (uint32_t)(k0 + i * T::B_ROWS_PER_LOAD) * (uint32_t)p.ldb * 2u);
+        }
       }
     };
     auto issue_tile = [&](int kt, int stage) {
@@ -1251,12 +1314,15 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-    } else if constexpr ((OUT == kOutF32Partial || OUT == kOutF32Accum) &&
+    } else if constexpr ((OUT == kOutF32Partial || OUT == kOutF32Accum ||
+                          OUT == kOutF32Atomic) &&
                          T::STAGED_F32_EPILOGUE) {
       // f32 C through LDS, one 32-row block of the wave tile at a time: the
       // prior C (C += A*B) is read and the result written as whole row
       // segments (F32_CPR lanes x 16 bytes per row) instead of 16-byte
-      // pieces of 32 rows.
+      // pieces of 32 rows. Atomic split-K adds each row segment with four
+      // buffer_atomic_add_f32, so one instruction's 64 lanes touch a few
+      // whole rows' cache lines rather than one line per lane.
       float *base = OUT == kOutF32Partial
                         ? p.ws + (size_t)part * (size_t)p.M * (size_t)p.ws_ld
                         : reinterpret_cast<float *>(p.C);
@@ -1282,7 +1348,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                        : kOob;
         }
         f32x4 old[OUT == kOutF32Accum ? NLD : 1];
-        if constexpr (OUT == kOutF32Accum) {
+        if constexpr (OUT == kOutF32Accum && !PRIOR_C_START) {
 #pragma unroll
           for (int t = 0; t < NLD; ++t)
             old[t] = __builtin_bit_cast(
@@ -1305,7 +1371,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
           f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
           if constexpr (OUT == kOutF32Accum) {
-            v += old[t];
+            if constexpr (!PRIOR_C_START)
+              v += old[t];
             if constexpr (EPI) {
               const epi_f32x4 b = epi_load_bias(ea, col, p.N);
 #pragma unroll
@@ -1313,12 +1380,19 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                 v[e] = epi_apply1(v[e], b[e], ea);
             }
           }
-          // f32 results (split-K partials, plain f32 C) are written once and
-          // not read again by this kernel: non-temporal, which leaves less
-          // dirty data in L2 for the kernel-end release (split-K 512^2 x
-          // 16384: 15.7 -> 15.1 us per GEMM); C += A*B keeps the default
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
-                                                 0, OUT == kOutF32Partial ? kStoreNT : 0);
+          if constexpr (OUT == kOutF32Atomic) {
+            // past the edges off[t] is kOob: the atomics are dropped
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v[e], rc, off[t] + 4u * e, 0, 0);
+          } else {
+            // f32 results (split-K partials, plain f32 C) are written once
+            // and not read again by this kernel: non-temporal, which leaves
+            // less dirty data in L2 for the kernel-end release (split-K 512^2
+            // x 16384: 15.7 -> 15.1 us per GEMM); C += A*B keeps the default
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
+                                                   0, OUT == kOutF32Partial ? kStoreNT : 0);
+          }
         }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {
@@ -1342,7 +1416,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int i0 = 0; i0 < TM; i0 += GI) {
         f32x4 old[GI][TN][4];
-        if constexpr (OUT == kOutF32Accum && !PREFETCH_C) {
+        if constexpr (OUT == kOutF32Accum && !PRIOR_C_START) {
 #pragma unroll
           for (int ii = 0; ii < GI; ++ii)
 #pragma unroll
@@ -1363,9 +1437,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
               f32x4 v = {acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
                          acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
               if constexpr (OUT == kOutF32Accum) {
-                if constexpr (PREFETCH_C)
-                  v += c_pre[i][j][g];
-                else
+                if constexpr (!PRIOR_C_START)
                   v += old[ii][j][g];
                 if constexpr (EPI) {
                   const epi_f32x4 b = epi_load_bias(ea, ccol_base + j * 32 + 8 * g, p.N);
@@ -1427,6 +1499,7 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
   using T = GemmTile<BM, BN, BK, WGM, WGN, STAGES>;
   constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
                 KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LPT = T::LPT;
+  static_assert(!T::IDLE_ROUNDS && !T::B_RAGGED_ROUNDS, "producer waves load whole rows per round");
   static_assert(T::STAGED_F32_EPILOGUE, "f32 partials staged through LDS");
   static_assert(KSTEPS == 4, "whole-k-tile fragment buffers sized for BK = 64");
   __shared__ u32x4 lds[STAGES * T::STAGE];

@@ -15,9 +15,10 @@
 // wherever the kernel template can run it:
 //  * the LDS ring fits 160 KiB and the wave tile holds at most 256
 //    accumulator registers per lane (16 tiles of 32x32);
-//  * every thread issues a whole number of 16-byte direct loads per operand
-//    per k-tile, and a lane's B swizzle phase is the same in every load round
-//    (so 1 wave cannot load 256-wide B rows);
+//  * an operand's k-tile is whole wavefronts' rounds of 16-byte direct loads
+//    (8 waves on a 32-deep k-tile of a 64- or 128-wide side leave whole
+//    waves idle in the last round), and a lane's B swizzle phase is the same
+//    in every load round (so 1 wave cannot load 256-wide B rows);
 //  * the loads a thread may have in flight at a wait fit the 6-bit vmcnt
 //    field (at most 63: 1 wave on 128x128x64 or 256x64x64 tiles stops at 3
 //    stages);
@@ -29,7 +30,8 @@
 // shapes with a list below (the Makefile reads these names)
 #define TBK_SHAPES(S)                                                           \
   S(64x64) S(64x128) S(128x64) S(128x128) S(64x256) S(256x64) S(128x256)       \
-      S(256x128) S(256x256) S(192x128)
+      S(256x128) S(256x256) S(192x128) S(192x64) S(192x256) S(64x192) S(128x192)   \
+          S(192x192) S(256x192)
 
 // Tiles whose plain f32-partial instance (output mode 1: split-K partials and
 // plain f32 C) is built with producer waves (gemm_kernel_pw: as many load-only
@@ -66,7 +68,8 @@
   X(64, 128, 64, 1, 4, 3), X(64, 128, 64, 1, 4, 4), \
   X(64, 128, 64, 2, 2, 2), X(64, 128, 64, 2, 2, 3), \
   X(64, 128, 64, 2, 4, 2), X(64, 128, 64, 2, 4, 3), \
-  X(64, 128, 64, 2, 4, 4)
+  X(64, 128, 64, 2, 4, 4), X(64, 128, 32, 2, 4, 2), \
+  X(64, 128, 32, 2, 4, 3), X(64, 128, 32, 2, 4, 4)
 
 #define TBK_TILES_128x64(X) \
   X(128, 64, 32, 1, 1, 2), X(128, 64, 32, 1, 1, 3), \
@@ -80,7 +83,8 @@
   X(128, 64, 64, 2, 2, 3), X(128, 64, 64, 4, 1, 2), \
   X(128, 64, 64, 4, 1, 3), X(128, 64, 64, 4, 1, 4), \
   X(128, 64, 64, 4, 2, 2), X(128, 64, 64, 4, 2, 3), \
-  X(128, 64, 64, 4, 2, 4)
+  X(128, 64, 64, 4, 2, 4), X(128, 64, 32, 4, 2, 2), \
+  X(128, 64, 32, 4, 2, 3), X(128, 64, 32, 4, 2, 4)
 
 #define TBK_TILES_128x128(X) \
   X(128, 128, 32, 1, 1, 2), X(128, 128, 32, 1, 1, 3), \
@@ -104,7 +108,8 @@
   X(64, 256, 64, 1, 2, 4), X(64, 256, 64, 1, 4, 2), \
   X(64, 256, 64, 1, 4, 3), X(64, 256, 64, 1, 4, 4), \
   X(64, 256, 64, 1, 8, 2), X(64, 256, 64, 1, 8, 3), \
-  X(64, 256, 64, 1, 8, 4)
+  X(64, 256, 64, 1, 8, 4), X(64, 256, 32, 1, 8, 2), \
+  X(64, 256, 32, 1, 8, 3), X(64, 256, 32, 1, 8, 4)
 
 #define TBK_TILES_256x64(X) \
   X(256, 64, 32, 1, 1, 2), X(256, 64, 32, 1, 1, 3), \
@@ -116,7 +121,9 @@
   X(256, 64, 64, 2, 1, 3), X(256, 64, 64, 2, 1, 4), \
   X(256, 64, 64, 4, 1, 2), X(256, 64, 64, 4, 1, 3), \
   X(256, 64, 64, 4, 1, 4), X(256, 64, 64, 8, 1, 2), \
-  X(256, 64, 64, 8, 1, 3), X(256, 64, 64, 8, 1, 4)
+  X(256, 64, 64, 8, 1, 3), X(256, 64, 64, 8, 1, 4), \
+  X(256, 64, 32, 8, 1, 2), X(256, 64, 32, 8, 1, 3), \
+  X(256, 64, 32, 8, 1, 4)
 
 #define TBK_TILES_128x256(X) \
   X(128, 256, 32, 1, 2, 2), X(128, 256, 32, 1, 2, 3), \
@@ -150,11 +157,54 @@
   X(192, 128, 32, 2, 1, 2), X(192, 128, 32, 2, 1, 3), \
   X(192, 128, 32, 2, 1, 4), X(192, 128, 32, 2, 2, 2), \
   X(192, 128, 32, 2, 2, 3), X(192, 128, 32, 2, 2, 4), \
-  X(192, 128, 64, 2, 1, 2), X(192, 128, 64, 2, 1, 3), \
-  X(192, 128, 64, 2, 1, 4), X(192, 128, 64, 2, 2, 2), \
-  X(192, 128, 64, 2, 2, 3), X(192, 128, 64, 2, 2, 4), \
-  X(192, 128, 64, 2, 4, 2), X(192, 128, 64, 2, 4, 3), \
-  X(192, 128, 64, 2, 4, 4)
+  X(192, 128, 32, 2, 4, 2), X(192, 128, 32, 2, 4, 3), \
+  X(192, 128, 32, 2, 4, 4), X(192, 128, 64, 2, 1, 2), \
+  X(192, 128, 64, 2, 1, 3), X(192, 128, 64, 2, 1, 4), \
+  X(192, 128, 64, 2, 2, 2), X(192, 128, 64, 2, 2, 3), \
+  X(192, 128, 64, 2, 2, 4), X(192, 128, 64, 2, 4, 2), \
+  X(192, 128, 64, 2, 4, 3), X(192, 128, 64, 2, 4, 4)
+
+// 192-row blocks on 64- and 256-wide B (96-row wave tiles: 3 MFMA tiles of
+// 32 per wave column)
+#define TBK_TILES_192x64(X) \
+  X(192, 64, 32, 1, 1, 2), X(192, 64, 32, 1, 1, 3), X(192, 64, 32, 1, 1, 4), \
+  X(192, 64, 32, 2, 1, 2), X(192, 64, 32, 2, 1, 3), X(192, 64, 32, 2, 1, 4), \
+  X(192, 64, 32, 2, 2, 2), X(192, 64, 32, 2, 2, 3), X(192, 64, 32, 2, 2, 4), \
+  X(192, 64, 64, 1, 1, 2), X(192, 64, 64, 1, 1, 3), \
+  X(192, 64, 64, 2, 1, 2), X(192, 64, 64, 2, 1, 3), X(192, 64, 64, 2, 1, 4), \
+  X(192, 64, 64, 2, 2, 2), X(192, 64, 64, 2, 2, 3), X(192, 64, 64, 2, 2, 4)
+
+#define TBK_TILES_192x256(X) \
+  X(192, 256, 32, 2, 2, 2), X(192, 256, 32, 2, 2, 3), X(192, 256, 32, 2, 2, 4), \
+  X(192, 256, 32, 2, 4, 2), X(192, 256, 32, 2, 4, 3), X(192, 256, 32, 2, 4, 4), \
+  X(192, 256, 64, 2, 2, 2), X(192, 256, 64, 2, 4, 2)
+
+// 192-wide B (384-byte rows: a load round ends inside a row, so each round
+// has its own lane offsets; B swizzle 2 rows per phase, 2 phases)
+#define TBK_TILES_64x192(X) \
+  X(64, 192, 32, 1, 1, 2), X(64, 192, 32, 1, 1, 3), X(64, 192, 32, 1, 1, 4), \
+  X(64, 192, 32, 1, 2, 2), X(64, 192, 32, 1, 2, 3), X(64, 192, 32, 1, 2, 4), \
+  X(64, 192, 32, 2, 2, 2), X(64, 192, 32, 2, 2, 3), X(64, 192, 32, 2, 2, 4), \
+  X(64, 192, 64, 1, 1, 2), X(64, 192, 64, 1, 1, 3), X(64, 192, 64, 1, 2, 2), \
+  X(64, 192, 64, 1, 2, 3), X(64, 192, 64, 1, 2, 4), X(64, 192, 64, 2, 2, 2), \
+  X(64, 192, 64, 2, 2, 3), X(64, 192, 64, 2, 2, 4)
+
+#define TBK_TILES_128x192(X) \
+  X(128, 192, 32, 1, 2, 2), X(128, 192, 32, 1, 2, 3), X(128, 192, 32, 1, 2, 4), \
+  X(128, 192, 32, 2, 2, 2), X(128, 192, 32, 2, 2, 3), X(128, 192, 32, 2, 2, 4), \
+  X(128, 192, 32, 4, 2, 2), X(128, 192, 32, 4, 2, 3), X(128, 192, 32, 4, 2, 4), \
+  X(128, 192, 64, 1, 2, 2), X(128, 192, 64, 1, 2, 3), X(128, 192, 64, 1, 2, 4), \
+  X(128, 192, 64, 2, 2, 2), X(128, 192, 64, 2, 2, 3), X(128, 192, 64, 2, 2, 4), \
+  X(128, 192, 64, 4, 2, 2), X(128, 192, 64, 4, 2, 3), X(128, 192, 64, 4, 2, 4)
+
+#define TBK_TILES_192x192(X) \
+  X(192, 192, 32, 2, 2, 2), X(192, 192, 32, 2, 2, 3), X(192, 192, 32, 2, 2, 4), \
+  X(192, 192, 64, 2, 2, 2), X(192, 192, 64, 2, 2, 3)
+
+#define TBK_TILES_256x192(X) \
+  X(256, 192, 32, 2, 2, 2), X(256, 192, 32, 2, 2, 3), X(256, 192, 32, 2, 2, 4), \
+  X(256, 192, 32, 4, 2, 2), X(256, 192, 32, 4, 2, 3), X(256, 192, 32, 4, 2, 4), \
+  X(256, 192, 64, 2, 2, 2), X(256, 192, 64, 4, 2, 2)
 
 // ---- the 16x16x32 loop (gemm_mfma16g.h) ------------------------------------
 // Tiles built on v_mfma_f32_16x16x32_f16 besides the hand-scheduled 4-wave

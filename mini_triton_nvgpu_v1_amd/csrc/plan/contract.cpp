@@ -5,6 +5,7 @@
 #include "serialize.h"
 
 #include <algorithm>
+#include <numeric>
 #include <set>
 #include <tuple>
 
@@ -171,8 +172,12 @@ static void checkKernelSwizzle(const KernelContract &k) {
   SharedSwizzle a = sharedSwizzle(encodingAttr(k.encodings, k.encodings.aShared, "a_shared"));
   SharedSwizzle b = sharedSwizzle(encodingAttr(k.encodings, k.encodings.bShared, "b_shared"));
   int64_t aPP = std::max<int64_t>(1, 256 / (c.blockK * 2)), aMax = c.blockK / 8;
-  int64_t bPP = std::max<int64_t>(1, 256 / (c.blockN * 2)),
-          bMax = std::min<int64_t>(4, c.blockN / 32);
+  // B: rows per phase 256 / gcd(row bytes, 256); phases the largest power of
+  // two dividing the 64-byte segments per row, at most 4 (GemmTile::B_PP,
+  // B_MAXPH)
+  const int64_t bSeg = c.blockN / 32;
+  int64_t bPP = 256 / std::gcd<int64_t>(c.blockN * 2, 256),
+          bMax = std::min<int64_t>(4, bSeg & -bSeg);
   // the 16x16x32 instance's B reads add the second XOR term (32-byte units,
   // phase (k / 8) % 2); the general loop has none
   const bool m16 = c.mmaKind == MmaKind::Mfma16x16x32F16;

@@ -157,7 +157,10 @@ InstanceSchedule instanceSchedule(const InstanceKey &k) {
   }
   const int64_t threads = k.wgm * k.wgn * 64;
   const int64_t nmfma = (k.bm / k.wgm / 32) * (k.bn / k.wgn / 32); // per 16-deep k step
-  const int64_t lpt = (k.bm * (k.bk / 8) + k.bk * (k.bn / 8)) / threads;
+  // whole load rounds per operand; a last round wider than the operand's
+  // stage leaves whole waves idle (they load zeros into a scratch row)
+  const int64_t lpt = (k.bm * (k.bk / 8) + threads - 1) / threads +
+                      (k.bk * (k.bn / 8) + threads - 1) / threads;
   s.loadsPerThread = lpt;
   if (k.out == kInstOutF32Partial && !k.epi && k.mfma == TB_MFMA_32X32X16 && producerTile(k)) {
     // the loaders issue with the compute waves' thread count: wave w - NW

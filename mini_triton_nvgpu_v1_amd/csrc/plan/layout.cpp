@@ -2,6 +2,7 @@
 #include "serialize.h"
 
 #include <algorithm>
+#include <numeric>
 #include <cstdlib>
 #include <limits>
 
@@ -89,6 +90,12 @@ std::pair<int64_t, int64_t> deriveWaveGrid(const KernelConfig &c, int64_t instrM
 //  * B ([block_k][block_n], read with transposing ds_read_b64_tr_b16, two
 //    16-lane groups covering 32 columns = 64 bytes of a row): 64 bytes,
 //    phases = min(256 / 64, 64-byte segments per row).
+// Rows per phase: rows before a row's bank offset repeats, period / gcd(row
+// bytes, period) (period / row bytes for power-of-two rows under the period,
+// 1 from the period up, 2 for 384-byte rows). Phases: at most period / unit
+// and a power of two dividing the units per row, so a unit XOR-ed with the
+// phase stays inside its row (the reference keeps it inside with a modulo,
+// LowerPipelineToNVGPU.cpp:1589-1621; a power of two needs none).
 static SharedSwizzle deriveSwizzle(const TargetInfo &t, int64_t rowBytes,
                                    int64_t unitBytes) {
   SharedSwizzle s;
@@ -97,8 +104,9 @@ static SharedSwizzle deriveSwizzle(const TargetInfo &t, int64_t rowBytes,
   if (rowBytes < unitBytes || rowBytes % unitBytes)
     return s;
   s.swizzlingByteWidth = unitBytes;
-  s.perPhase = std::max<int64_t>(1, period / rowBytes);
-  s.maxPhase = std::max<int64_t>(1, std::min(rowBytes / unitBytes, period / unitBytes));
+  s.perPhase = period / std::gcd(rowBytes, period);
+  const int64_t units = rowBytes / unitBytes;
+  s.maxPhase = std::max<int64_t>(1, std::min(units & -units, period / unitBytes));
   return s;
 }
 

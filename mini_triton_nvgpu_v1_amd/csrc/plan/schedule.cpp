@@ -584,15 +584,17 @@ template <class V> void fields(V &v, AsyncPlan &p) {
 }
 
 // Loads one thread issues per k group: each 16-byte vector of the A and B
-// tiles is one buffer_load_dwordx4 ... lds, spread over the workgroup.
+// tiles is one buffer_load_dwordx4 ... lds, spread over the workgroup in
+// rounds of one vector per lane. An operand's vectors are whole waves' rounds;
+// when they do not fill the last round, the waves past them still issue that
+// load (zeros into a scratch row of LDS), so every lane issues the same count.
 static int64_t loadsPerThread(const KernelConfig &c, const TransportPlan &tr) {
   int64_t threads = c.numWarps * 64;
-  int64_t vecs = tr.operandA.transactionBytes / tr.operandA.asyncVectorBytes +
-                 tr.operandB.transactionBytes / tr.operandB.asyncVectorBytes;
-  if (vecs % threads)
-    throw Error("A/B tiles must split evenly into 16-byte loads over the "
-                "workgroup's lanes");
-  return vecs / threads;
+  int64_t va = tr.operandA.transactionBytes / tr.operandA.asyncVectorBytes;
+  int64_t vb = tr.operandB.transactionBytes / tr.operandB.asyncVectorBytes;
+  if (va % 64 || vb % 64)
+    throw Error("A/B tiles must split into whole wavefront rounds of 16-byte loads");
+  return (va + threads - 1) / threads + (vb + threads - 1) / threads;
 }
 
 // Reference: AsyncPlan.cpp:543-843 (one producer group per stage-owned
