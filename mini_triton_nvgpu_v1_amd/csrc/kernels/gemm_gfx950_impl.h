@@ -902,13 +902,17 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
 
     f32x16 acc[TM][TN];
     // C += A*B on small wave tiles of 4-wave workgroups (512 registers per
-    // lane): the prior C is the accumulators' starting value, as in the
-    // reference (LowerPipelineToNVGPU.cpp:2246-2263, C loaded into the
-    // accumulators before the K loop; the sum is C + a0 b0 + a1 b1 + ... in
-    // k order). Its loads are issued before the tile's first A/B loads, so
-    // their latency runs beside those loads, and the first MFMA (which waits
-    // for k-tile 0) finds them landed.
-    constexpr bool PRIOR_C_START = OUT == kOutF32Accum && TM * TN <= 4 && NW <= 4;
+    // lane) whose f32 result is not staged through LDS: the prior C is the
+    // accumulators' starting value, as in the reference
+    // (LowerPipelineToNVGPU.cpp:2246-2263: C loaded into the accumulators
+    // before the K loop; the sum is C + a0 b0 + a1 b1 + ... in k order),
+    // loaded in their layout before the tile's first A/B loads, so its
+    // latency runs beside theirs (the first MFMA waits for k-tile 0, issued
+    // after it). Staged tiles read it after the loop as whole rows (fewer,
+    // wider requests; loaded first, as rows or in the accumulator layout, it
+    // measured no faster for the reference's small cases, which run out of L2).
+    constexpr bool PRIOR_C_START = OUT == kOutF32Accum && !T::STAGED_F32_EPILOGUE &&
+                                   TM * TN <= 4 && NW <= 4;
     if constexpr (PRIOR_C_START) {
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
@@ -1348,7 +1352,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                        : kOob;
         }
         f32x4 old[OUT == kOutF32Accum ? NLD : 1];
-        if constexpr (OUT == kOutF32Accum && !PRIOR_C_START) {
+        if constexpr (OUT == kOutF32Accum) {
 #pragma unroll
           for (int t = 0; t < NLD; ++t)
             old[t] = __builtin_bit_cast(
@@ -1371,8 +1375,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
           const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
           f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
           if constexpr (OUT == kOutF32Accum) {
-            if constexpr (!PRIOR_C_START)
-              v += old[t];
+            v += old[t];
             if constexpr (EPI) {
               const epi_f32x4 b = epi_load_bias(ea, col, p.N);
 #pragma unroll
