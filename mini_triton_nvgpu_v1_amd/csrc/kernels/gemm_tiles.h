@@ -216,34 +216,42 @@
 // (The hand-scheduled tile's partial-K build is this loop too, instantiated
 // with its entries. 8 waves of 64x128 on 256x256 do not fit their 256
 // registers per wave and are not listed.) The lists cover the 4- and 8-wave
-// picks of the common blocks, and at block_k 64
-// the wave tiles of 128x128 (1 wave on 128x128, 2 on 256x128 / 128x256),
-// 256x64 (1 wave) and 96x128 (2 waves on 192x128) whose 32x32x16 builds
-// spill. Wave tiles of 48 or 64 MFMA tiles are listed at block_k 64 only:
-// with 32-deep k-tiles the fragment buffer of the last k-tile depends on
-// the k-tile count's parity, and with 192-256 accumulator registers held
-// the compiler spills at the two tails' merge.
-#define TBK_M16_SHAPES(S) S(128x128) S(256x128) S(128x256) S(256x64) S(192x128) S(256x256)
+// picks of the common blocks, and the wave tiles whose 32x32x16 builds
+// spill: 128x128 (1 wave on 128x128, 2 on 256x128 / 128x256), 256x64 and
+// 192x64 (1 wave) and 96x128 (2 waves on 192x128), at block_k 32 and 64
+// wherever the prologue's loads (every stage's k-tile) fit the 6-bit vmcnt.
+// 32-deep k-tiles run whole k-tile bodies with no tail, so their wave tiles
+// of 48 or 64 MFMA tiles hold their accumulators without a merge.
+#define TBK_M16_SHAPES(S)                                                              \
+  S(128x128) S(256x128) S(128x256) S(256x64) S(192x128) S(256x256) S(192x64)
 
 #define TBK_M16_TILES_128x128(X) \
   X(128, 128, 64, 2, 2, 2), X(128, 128, 64, 2, 2, 3), X(128, 128, 64, 2, 2, 4), \
   X(128, 128, 32, 2, 2, 2), X(128, 128, 32, 2, 2, 3), X(128, 128, 32, 2, 2, 4), \
-  X(128, 128, 64, 1, 1, 2)
+  X(128, 128, 64, 1, 1, 2), \
+  X(128, 128, 32, 1, 1, 2), X(128, 128, 32, 1, 1, 3), X(128, 128, 32, 1, 1, 4)
 
 #define TBK_M16_TILES_256x128(X) \
   X(256, 128, 64, 4, 1, 2), X(256, 128, 64, 4, 1, 3), \
   X(256, 128, 32, 4, 1, 2), X(256, 128, 32, 4, 1, 3), X(256, 128, 32, 4, 1, 4), \
   X(256, 128, 64, 4, 2, 2), X(256, 128, 64, 4, 2, 3), \
-  X(256, 128, 64, 2, 1, 2), X(256, 128, 64, 2, 1, 3)
+  X(256, 128, 64, 2, 1, 2), X(256, 128, 64, 2, 1, 3), \
+  X(256, 128, 32, 2, 1, 2), X(256, 128, 32, 2, 1, 3), X(256, 128, 32, 2, 1, 4)
 
 #define TBK_M16_TILES_128x256(X) \
   X(128, 256, 64, 1, 4, 2), X(128, 256, 64, 1, 4, 3), \
   X(128, 256, 32, 1, 4, 2), X(128, 256, 32, 1, 4, 3), X(128, 256, 32, 1, 4, 4), \
   X(128, 256, 64, 2, 4, 2), X(128, 256, 64, 2, 4, 3), \
-  X(128, 256, 64, 1, 2, 2), X(128, 256, 64, 1, 2, 3)
+  X(128, 256, 64, 1, 2, 2), X(128, 256, 64, 1, 2, 3), \
+  X(128, 256, 32, 1, 2, 2), X(128, 256, 32, 1, 2, 3), X(128, 256, 32, 1, 2, 4)
 
 
-#define TBK_M16_TILES_256x64(X) X(256, 64, 64, 1, 1, 2)
+#define TBK_M16_TILES_256x64(X) \
+  X(256, 64, 64, 1, 1, 2), X(256, 64, 32, 1, 1, 2), X(256, 64, 32, 1, 1, 3), \
+  X(256, 64, 32, 1, 1, 4)
+
+// one wave of 192x64 (its 32x32x16 build spills)
+#define TBK_M16_TILES_192x64(X) X(192, 64, 64, 1, 1, 2)
 
 // 4 waves of 128x128 on 256x256 with 32-deep k-tiles in 3 or 4 LDS stages
 // (the same 128 KiB ring as the hand-scheduled 64-deep 2-stage tile, cut
