@@ -985,7 +985,8 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         const int i = l;
         const int lc = a_lchunk(i);
         // wave-uniform: the round's chunks of this wave lie inside the stage
-        const bool live = (i * NW + wave) * 64 < T::A_STAGE;
+        // (always, unless the tile has a partial round)
+        const bool live = !T::IDLE_ROUNDS || (i * NW + wave) * 64 < T::A_STAGE;
         const bool ok = live && kt_ok && (k0 + lc * 8) < p.K &&
                         i * T::A_ROWS_PER_LOAD < a_rows_left;
         load_lds16(ra4, live ? a_lds + i * NW * 1024u : idle_lds,
@@ -994,7 +995,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       } else {
         const int i = l - LA;
         const uint32_t b_lds = a_lds + T::A_STAGE * 16u;
-        const bool live = (i * NW + wave) * 64 < T::B_STAGE;
+        const bool live = !T::IDLE_ROUNDS || (i * NW + wave) * 64 < T::B_STAGE;
         if constexpr (T::B_RAGGED_ROUNDS) {
           // the round's rows ride in the vector offset; the k-tile's in the
           // scalar one (unsigned: see below)
