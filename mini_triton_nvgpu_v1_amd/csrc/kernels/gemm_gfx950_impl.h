@@ -913,6 +913,14 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
     // measured no faster for the reference's small cases, which run out of L2).
     constexpr bool PRIOR_C_START = OUT == kOutF32Accum && !T::STAGED_F32_EPILOGUE &&
                                    TM * TN <= 4 && NW <= 4;
+    // The staged small tiles load their prior C as the epilogue's whole rows
+    // right after the prologue's A/B loads: k-tile 0 arrives first, and the
+    // prior C during the first k-tiles' MFMAs instead of after the loop.
+    constexpr int NLD32 = 32 / T::F32_RPI; // staged row segments per lane per 32-row block
+    constexpr bool C_ROWS_EARLY = OUT == kOutF32Accum && T::STAGED_F32_EPILOGUE &&
+                                  TM * TN <= 4 && NW <= 4 &&
+                                  T::VM_PROLOGUE + TM * NLD32 < 64;
+    f32x4 c_rows[C_ROWS_EARLY ? TM : 1][C_ROWS_EARLY ? NLD32 : 1];
     if constexpr (PRIOR_C_START) {
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
@@ -1097,7 +1105,28 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       for (int st = 0; st < STAGES; ++st)
         issue_tile(kt0 + st, st);
     }
-    wait_vmcnt<T::VM_PROLOGUE>();
+    if constexpr (C_ROWS_EARLY) {
+      const __amdgpu_buffer_rsrc_t rc =
+          make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
+      const int col = n0 + wn * T::WTN + 4 * (lane % T::F32_CPR);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int t = 0; t < NLD32; ++t) {
+          const int row = m0 + wm * T::WTM + i * 32 + t * T::F32_RPI + lane / T::F32_CPR;
+          const uint32_t off =
+              (row < p.M && col < p.N)
+                  ? ((uint32_t)(row - m0) * (uint32_t)p.ldc + (uint32_t)col) * 4u
+                  : kOob;
+          c_rows[i][t] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, 0));
+        }
+      // the prior C loads are the youngest: k-tile 0 has landed once at most
+      // VM_PROLOGUE of the A/B loads and all of them are outstanding
+      wait_vmcnt<T::VM_PROLOGUE + TM * NLD32>();
+    } else {
+      wait_vmcnt<T::VM_PROLOGUE>();
+    }
     __syncthreads();
     read_frags(0, 0, 0);
 
@@ -1353,7 +1382,11 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
                        : kOob;
         }
         f32x4 old[OUT == kOutF32Accum ? NLD : 1];
-        if constexpr (OUT == kOutF32Accum) {
+        if constexpr (C_ROWS_EARLY) {
+#pragma unroll
+          for (int t = 0; t < NLD; ++t)
+            old[t] = c_rows[i][t];
+        } else if constexpr (OUT == kOutF32Accum) {
 #pragma unroll
           for (int t = 0; t < NLD; ++t)
             old[t] = __builtin_bit_cast(
