@@ -585,20 +585,73 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // k step 1, slots LO .. HI-1
-  auto kstep1 = [&](auto lo_c, auto hi_c) {
+  // k step 1, slots LO .. HI-1, `extra` per slot
+  auto kstep1x = [&](auto lo_c, auto hi_c, auto &&extra) {
     static_for<64>([&](auto m_c) {
       constexpr int m = decltype(m_c)::value;
       if constexpr (m >= decltype(lo_c)::value && m < decltype(hi_c)::value) {
         mfma(1, m, false);
+        extra(m);
         __builtin_amdgcn_sched_barrier(0);
       }
     });
   };
+  auto kstep1 = [&](auto lo_c, auto hi_c) { kstep1x(lo_c, hi_c, [](int) {}); };
   using Z = std::integral_constant<int, 0>;
   using Q = std::integral_constant<int, BQ>;
   using E = std::integral_constant<int, 64>;
   auto nothing = [](int) {};
+
+  // f32 C += A*B: the prior C is added into the accumulators during the
+  // first 16 loop bodies instead of after the loop, so its 64 MB (at 4096^3)
+  // are read while the main loop leaves HBM mostly idle, not after it. Body q
+  // (k-tiles q and q+1) adds the prior C of tiles 4q .. 4q+3 (MFMA order
+  // m = 8i + j), loaded one body ahead (body 0's in the prologue) in the
+  // accumulator layout (16 bytes per lane per tile: lane l holds row 16i + l %
+  // 16, columns 16j + 4(l / 16) .. +3). Tile m's add sits 8 MFMA slots after
+  // its MFMA in the body's first k step (slot m + 8, or slot m - 56 of the
+  // next k step for m >= 56): its accumulators are no MFMA's operand from 8
+  // slots before the add (128+ cycles, past rule (b)'s 24 wait states) to 48
+  // slots after it. The loads are ordinary buffer loads; each body's barrier
+  // (vmcnt(0)) has them landed before the next body adds them. Whole tiles
+  // of at least 18 k-tiles only; the others add the prior C in the epilogue.
+  constexpr bool C_IN_LOOP = OUT == kOutF32Accum;
+  const bool c_in_loop = C_IN_LOOP && nk >= 18 && m0 + 256 <= p.M && n0 + 256 <= p.N;
+  f32x4 cbuf[C_IN_LOOP ? 2 : 1][4];
+  const __amdgpu_buffer_rsrc_t rcc =
+      make_rsrc(rows_at(p.C, m0, p.ldc, 4), rows_bytes(m0, p.M, p.ldc, 4));
+  const uint32_t c_voff = ((uint32_t)(wm * 128 + (lane & 15)) * (uint32_t)p.ldc +
+                           (uint32_t)(n0 + wn * 128 + 4 * (lane >> 4))) * 4u;
+  auto c_load = [&](auto q_c) {
+    constexpr int q = decltype(q_c)::value;
+    static_for<4>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value, mm = 4 * q + t;
+      cbuf[q & 1][t] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rcc, c_voff, (int)((uint32_t)(16 * (mm >> 3)) * (uint32_t)p.ldc * 4u +
+                                        64u * (mm & 7)),
+                     0));
+    });
+  };
+  // the add of body q at slot s of its first k step (s < 64) or of the next
+  // (s - 64): tile s - 8
+  auto c_add = [&](auto q_c, int s) {
+    constexpr int q = decltype(q_c)::value;
+    static_for<4>([&](auto t_c) {
+      constexpr int t = decltype(t_c)::value, mm = 4 * q + t;
+      if (s == mm + 8) {
+        acc[mm >> 3][mm & 7] += cbuf[q & 1][t];
+        // the sum back in its AGPRs in this slot: left to the compiler, the
+        // v_accvgpr_write sinks to right before the tile's next asm MFMA,
+        // which then reads srcC without the VALU-write wait states
+        asm volatile("" : "+a"(acc[mm >> 3][mm & 7]));
+      }
+    });
+  };
+  if constexpr (C_IN_LOOP) {
+    if (c_in_loop)
+      c_load(std::integral_constant<int, 0>{});
+  }
 
   // prologue: k-tiles 0 and 1 in flight, wait for 0, run it up to its barrier
   {
@@ -622,7 +675,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
 
   // body(it): k-tile it (stage S) from its barrier on, k-tile it+1 (stage
   // S^1) up to its barrier; stage S is refilled with k-tile it+2.
-  auto body = [&](int it, auto stage) {
+  auto body_h = [&](int it, auto stage, auto &&start, auto &&k0, auto &&k1) {
     constexpr int S = decltype(stage)::value, Sn = S ^ 1;
     const bool ok = it + 2 < nk;
     const u32x4 ra = rsrc_dwords(a_tile, ok ? a_bytes : 0u);
@@ -633,6 +686,7 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     static_assert(kMfma16VmLoop == 0 && kMfma16LgkmLoop == 0, "barrier wait below");
     wait_vmcnt_lgkm0<kMfma16VmLoop>();
     barrier();
+    start();
     static_for<64 - BQ>([&](auto s_c) {
       constexpr int m = BQ + decltype(s_c)::value;
       mfma(1, m, false);
@@ -651,11 +705,31 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     auto refill = [&](int m) {
       if (m >= OFF && ((m - OFF) % LS) == 0 && NB + (m - OFF) / LS < 16)
         load(ra, rb, it + 2, stage, NB + (m - OFF) / LS);
+      k0(m);
     };
     kstep0(Sn, refill, false);
-    kstep1(Z{}, Q{});
+    kstep1x(Z{}, Q{}, k1);
+  };
+  auto body = [&](int it, auto stage) {
+    auto none = [](int) {};
+    body_h(it, stage, []() {}, none, none);
   };
   int it = 0;
+  if constexpr (C_IN_LOOP) {
+    if (c_in_loop) { // nk >= 18: bodies 0 .. 15, then the loop from k-tile 16
+      static_for<16>([&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        body_h(
+            q, std::integral_constant<int, q & 1>{},
+            [&]() {
+              if constexpr (q + 1 < 16)
+                c_load(std::integral_constant<int, q + 1>{});
+            },
+            [&](int m) { c_add(q_c, m); }, [&](int m) { c_add(q_c, m + 64); });
+      });
+      it = 16;
+    }
+  }
   for (; it + 2 <= nk - 1; it += 2) {
     body(it, S0{});
     body(it + 1, S1{});
@@ -776,10 +850,12 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
     f32x4 old[OUT == kOutF32Accum ? PF : 1][8];
     auto load_old = [&](int i) {
       if constexpr (OUT == kOutF32Accum) {
+        if (!c_in_loop) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          old[i % PF][t] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, c_off(i, t), 0, 0));
+          for (int t = 0; t < 8; ++t)
+            old[i % PF][t] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, c_off(i, t), 0, 0));
+        }
       }
     };
 #pragma unroll
@@ -807,8 +883,10 @@ __device__ __forceinline__ void mfma16_tile(const GemmParams &p, int m0, int n0,
       for (int t = 0; t < 8; ++t) {
         const int rr = 2 * t + hr;
         f32x4 v = *(const TBK_LDS f32x4 *)(blk + rr * 512 + ((q ^ rr) * 16));
-        if constexpr (OUT == kOutF32Accum)
-          v += old[i % PF][t];
+        if constexpr (OUT == kOutF32Accum) {
+          if (!c_in_loop)
+            v += old[i % PF][t];
+        }
         if constexpr (EPI) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)

@@ -14,7 +14,10 @@ and without the fused steps, on any M, N and K. Checks:
   (with and without the fused steps), and C += A*B on a zero C equals the
   plain f32 C;
 * bit for bit against the 32x32x16 general loop on the same tile (same f32
-  sums in the same k order, the prior C added after the sum in both);
+  sums in the same k order, the prior C added after the sum in both) for K
+  of fewer than 18 k-tiles; from 18 k-tiles on, whole tiles add the prior C
+  inside the main loop, checked against the plain f32 C plus the prior C to
+  f32 rounding;
 * run-to-run bit-identity.
 """
 import numpy as np
@@ -162,6 +165,55 @@ def test_f32_c_fused_steps(steps, device):
     same = np.array_equal(half.view(np.uint16), plain.astype(np.float16).view(np.uint16))
     print(f"f16 C + steps == f32 C + steps rounded: {same}", flush=True)
     assert same
+
+
+# K of at least 18 k-tiles: whole tiles add the prior C inside the main loop
+# (during its first 16 bodies), ragged tiles and shorter K after the loop
+LONG_K = [
+    (520, 392, 1200, tb.MAP_GROUPED_TILE, None, 8),       # 19 k-tiles, partial last; 2 whole
+    (512, 768, 1152, tb.MAP_PERSISTENT_GROUPED, 4, 0),    # exactly 18; 6 tiles on 4 programs
+    (512, 512, 1088, tb.MAP_TILE, None, 0),               # 17: the prior C after the loop
+]
+
+
+@pytest.mark.parametrize("case", LONG_K, ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}_m{c[3]}")
+def test_f32_accumulate_long_k(case, device):
+    """C += A*B where the prior C joins the sum inside the main loop: against
+    the fp64 oracle; against the plain f32 C plus the prior C to f32 rounding
+    (a prior C added twice or not at all is off by the prior C itself);
+    exactly the plain f32 C on a zero C; run-to-run identical; and, where
+    the add comes after the loop (fewer than 18 k-tiles), bit for bit the
+    32x32x16 general loop."""
+    M, N, K, mapping, programs, pad = case
+    print(f"case {case}", flush=True)
+    A, B = oracle.config_inputs(M, N, K, 0x5EED1000 + M + N + K, oracle.UNIFORM)
+    dA, dB = torch.from_numpy(A).to(device), torch.from_numpy(B).to(device)
+    init = np.full((M, N + pad), 7.0, np.float32)
+    init[:, :N] = np.random.default_rng(K).uniform(-1, 1, (M, N)).astype(np.float32)
+    acc = _run(_cfg(M, N, K, 2, mapping, programs, pad), dA, dB, init=init)
+    ref = oracle.gemm_f64(A, B, init=np.ascontiguousarray(init[:, :N]))
+    bad, err, worst = oracle.check_tolerance(np.ascontiguousarray(acc[:, :N]), ref, rtol=RTOL)
+    print(f"C += A*B: violations={bad} max|err|={err:.3e}", flush=True)
+    assert bad == 0, f"{bad} elements outside tolerance; worst {err} at {worst}"
+    assert (acc[:, N:] == 7.0).all(), "padding columns written"
+
+    plain = _run(_cfg(M, N, K, 1, mapping, programs, pad), dA, dB)[:, :N]
+    sum_ = plain.astype(np.float64) + init[:, :N]
+    scale = np.abs(plain).astype(np.float64) + np.abs(init[:, :N]) + 1.0
+    off = np.abs(acc[:, :N] - sum_) > 1e-4 * scale
+    print(f"C += A*B vs plain + C: {int(off.sum())} off", flush=True)
+    assert not off.any(), f"{int(off.sum())} elements differ from plain f32 C + prior C"
+
+    again = _run(_cfg(M, N, K, 2, mapping, programs, pad), dA, dB, init=init)
+    assert np.array_equal(acc.view(np.uint32), again.view(np.uint32)), "not run-to-run identical"
+    zero = _run(_cfg(M, N, K, 2, mapping, programs, pad), dA, dB,
+                init=np.zeros((M, N + pad), np.float32))
+    assert np.array_equal(zero[:, :N], plain), "C += A*B on a zero C != plain f32 C"
+    if -(-K // 64) < 18:
+        general = _run(_cfg(M, N, K, 2, mapping, programs, pad, mfma=tb.MFMA_32X32X16),
+                       dA, dB, init=init)
+        assert np.array_equal(general.view(np.uint32), acc.view(np.uint32)), \
+            "C += A*B differs from the general loop's"
 
 
 def test_f32_accumulate_4096(device):
