@@ -173,6 +173,7 @@ LONG_K = [
     (520, 392, 1200, tb.MAP_GROUPED_TILE, None, 8),       # 19 k-tiles, partial last; 2 whole
     (512, 768, 1152, tb.MAP_PERSISTENT_GROUPED, 4, 0),    # exactly 18; 6 tiles on 4 programs
     (512, 512, 1088, tb.MAP_TILE, None, 0),               # 17: the prior C after the loop
+    (1024, 1024, 1608, tb.MAP_PERSISTENT_TILE, 5, 0),     # 26, partial last; 16 tiles on 5
 ]
 
 
