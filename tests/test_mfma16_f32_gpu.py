@@ -134,9 +134,12 @@ STEPS = [(tb.EPI_BIAS_F32, tb.ACT_GELU_TANH, 3, -0.5, 1.5),
          (tb.EPI_BIAS_NONE, tb.ACT_RELU, 2, 0.0, 2.0)]
 
 
+# K = 1200 (19 k-tiles): the whole tiles add the prior C inside the main loop,
+# the steps then run on C + A*B in the epilogue
+@pytest.mark.parametrize("K", [200, 1200])
 @pytest.mark.parametrize("steps", STEPS, ids=lambda s: f"bias{s[0]}_act{s[1]}_clamp{s[2]}")
-def test_f32_c_fused_steps(steps, device):
-    M, N, K = 520, 392, 200
+def test_f32_c_fused_steps(steps, K, device):
+    M, N = 520, 392
     kind, act, bits, lo, hi = steps
     A, B = oracle.config_inputs(M, N, K, 0x5EED0F80 + act, oracle.UNIFORM)
     dA, dB = torch.from_numpy(A).to(device), torch.from_numpy(B).to(device)
