@@ -9,6 +9,13 @@ Runs, on one stream and in this order:
 Usage (under rocprofv3, the program after `--`):
   rocprofv3 --pmc FETCH_SIZE -d out/pmc -- \
       python3 -m mini_triton_nvgpu_v1_amd.profiling --workload gemm_4096
+
+`--small-tiles` instead launches single-tile problems of the reference's
+small cases (64x64, 64x128 and 128x64 tiles on the wave counts its configs
+name, and the 64x64 tile on 4 waves beside its 1) as f16 C, plain f32 C and
+f32 C += A*B, `--reps` times each, back to back: a kernel trace of it shows
+what the output mode and the wave count cost at the size where a launch is
+all latency.
 """
 from __future__ import annotations
 
@@ -24,6 +31,8 @@ def main() -> int:
     ap.add_argument("--copy-reps", type=int, default=3)
     ap.add_argument("--hipblaslt", action="store_true",
                     help="also run torch.matmul on the same operands")
+    ap.add_argument("--small-tiles", action="store_true",
+                    help="single-tile problems of the reference's small cases")
     args = ap.parse_args()
 
     import torch
@@ -33,6 +42,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
+    if args.small_tiles:
+        return small_tiles(tb, torch, dev, stream, args.reps)
     n = args.copy_mib * 1024 * 1024
     src = torch.ones(n, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
@@ -67,6 +78,37 @@ def main() -> int:
             torch.matmul(A, B, out=C)
         torch.cuda.synchronize()
         print(f"profiling: {args.reps} torch.matmul (hipBLASLt) launches", flush=True)
+    return 0
+
+
+# (M, N, K, block_m, block_n, block_k, wave grid m, wave grid n): one tile each
+SMALL_TILES = [(64, 64, 32, 64, 64, 32, 1, 1), (64, 64, 32, 64, 64, 32, 2, 2),
+               (64, 64, 64, 64, 64, 32, 1, 1), (64, 64, 64, 64, 64, 64, 1, 1),
+               (128, 64, 32, 128, 64, 32, 4, 1), (64, 128, 32, 64, 128, 32, 1, 4)]
+
+
+def small_tiles(tb, torch, dev, stream, reps) -> int:
+    for (M, N, K, bm, bn, bk, gm, gn) in SMALL_TILES:
+        A = torch.empty((M, K), dtype=torch.float16, device=dev)
+        B = torch.empty((K, N), dtype=torch.float16, device=dev)
+        tb.fill_seeded_f16(A, M, K, 0x5EED0A00 + K, 0, 1.0, stream=stream)
+        tb.fill_seeded_f16(B, K, N, 0x5EED0B00 + N, 0, 1.0, stream=stream)
+        for out in (0, 1, 2):  # f16 C, plain f32 C, f32 C += A*B
+            cfg = tb.GemmConfig(
+                m=M, n=N, k=K, lda=K, ldb=N, ldc=N,
+                c_dtype=tb.DTYPE_F16 if out == 0 else tb.DTYPE_F32,
+                acc_init=tb.ACC_INIT_LOAD_C if out == 2 else tb.ACC_INIT_ZERO,
+                block_m=bm, block_n=bn, block_k=bk, num_waves=gm * gn, wave_grid_m=gm,
+                wave_grid_n=gn, stages=2, mapping=tb.MAP_TILE, group_m=1, split_k=1,
+                reduction=tb.RED_NONE, num_programs=1, xcd_remap=0, mfma=tb.MFMA_32X32X16)
+            desc = tb.GemmDesc.from_config(cfg)
+            C = torch.zeros((M, N), dtype=torch.float16 if out == 0 else torch.float32,
+                            device=dev)
+            for _ in range(reps):
+                desc.launch(A, B, C, stream=stream)
+            torch.cuda.synchronize()
+            print(f"profiling: {reps} launches of {desc.kernel_name} ({M}x{N}x{K})",
+                  flush=True)
     return 0
 
 
