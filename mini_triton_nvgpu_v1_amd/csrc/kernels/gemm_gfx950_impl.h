@@ -342,8 +342,14 @@ struct GemmTile {
   static constexpr int F32_RPP = F32_ROWB >= 256 ? 1 : 256 / F32_ROWB;
   static constexpr int F32_XOR = F32_CPR < 16 ? F32_CPR : 16;
   static constexpr int F32_RPI = 64 / F32_CPR;             // rows per 64-lane read
+  // A 32-row block of every wave that does not fit the ring (4 waves of 32 x
+  // 64 on a 24 KiB ring) goes through in two 16-row halves: in each, the
+  // lanes holding that half's rows write, and every lane reads back.
+  static constexpr bool F32_HALF_BLOCKS =
+      NW * 32 * F32_ROWB > LDS_BYTES && NW * 16 * F32_ROWB <= LDS_BYTES;
+  static constexpr int F32_BLOCK_ROWS = F32_HALF_BLOCKS ? 16 : 32; // rows per LDS pass
   static constexpr bool STAGED_F32_EPILOGUE =
-      (WTN == 32 || WTN == 64 || WTN == 128) && NW * 32 * F32_ROWB <= LDS_BYTES;
+      (WTN == 32 || WTN == 64 || WTN == 128) && NW * F32_BLOCK_ROWS * F32_ROWB <= LDS_BYTES;
 
   static_assert(BM % (WGM * 32) == 0 && BN % (WGN * 32) == 0, "wave tile");
   static_assert(KSTEPS == 2 || KSTEPS == 4, "BK must be 32 or 64");
@@ -1442,9 +1448,12 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
       const __amdgpu_buffer_rsrc_t rc =
           make_rsrc(rows_at(base, m0, ld, 4), rows_bytes(m0, p.M, ld, 4));
       __syncthreads(); // every wave drained its loads and finished its reads
+      constexpr int BR = T::F32_BLOCK_ROWS, HB = 32 / BR; // rows per pass, passes
       TBK_LDS char *wl =
-          (TBK_LDS char *)(TBK_LDS void *)lds + wave * (32 * T::F32_ROWB);
+          (TBK_LDS char *)(TBK_LDS void *)lds + wave * (BR * T::F32_ROWB);
       constexpr int NLD = 32 / T::F32_RPI; // row segments per lane per block
+      constexpr int NLDH = NLD / HB;       // per pass
+      static_assert(BR % T::F32_RPI == 0, "a pass reads whole rows");
       const int q = lane % T::F32_CPR;
       const int col = n0 + wn * T::WTN + 4 * q;
       const int rw = lane & 31;
@@ -1470,20 +1479,35 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
             old[t] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, off[t], 0, 0));
         }
-        // accumulators in: lane l holds row l % 32, columns 32j + 8g + 4(l / 32)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+        for (int h = 0; h < HB; ++h) {
+        // accumulators in: lane l holds row l % 32, columns 32j + 8g + 4(l / 32);
+        // in pass h only the lanes of rows h BR .. h BR + BR - 1 (row rw % BR
+        // of the pass region). The lanes read what other lanes wrote, which
+        // the compiler's one-thread memory model does not see: a lane that
+        // skipped this pass's writes would reuse its previous pass's read of
+        // the same address (measured: the reads moved into the masked write
+        // block). The memory clobbers make every lane read after the writes
+        // (LDS executes one wave's operations in order; no instruction).
+        asm volatile("" ::: "memory");
+        if (HB == 1 || rw / BR == h) {
+          const int rl = rw % BR;
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int cs = (8 * j + 2 * g + khalf) ^ ((rw / T::F32_RPP) % T::F32_XOR);
-            *(TBK_LDS f32x4 *)(wl + rw * T::F32_ROWB + cs * 16) =
-                (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
-                        acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-          }
-        // whole row segments out
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int t = 0; t < NLD; ++t) {
-          const int r = t * T::F32_RPI + lane / T::F32_CPR;
+            for (int g = 0; g < 4; ++g) {
+              const int cs = (8 * j + 2 * g + khalf) ^ ((rl / T::F32_RPP) % T::F32_XOR);
+              *(TBK_LDS f32x4 *)(wl + rl * T::F32_ROWB + cs * 16) =
+                  (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
+                          acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+            }
+        }
+        asm volatile("" ::: "memory");
+        // whole row segments out: segment t of the block is row t F32_RPI +
+        // l / F32_CPR, in pass t / NLDH
+#pragma unroll
+        for (int t = h * NLDH; t < (h + 1) * NLDH; ++t) {
+          const int r = (t - h * NLDH) * T::F32_RPI + lane / T::F32_CPR; // row in the pass
           const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
           f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
           if constexpr (OUT == kOutF32Accum) {
@@ -1508,6 +1532,7 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
                                                    0, OUT == kOutF32Partial ? kStoreNT : 0);
           }
+        }
         }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {
@@ -1615,7 +1640,8 @@ __global__ __launch_bounds__(2 * WGM * WGN * 64, 1) void gemm_kernel_pw(GemmPara
   constexpr int NW = T::NW, KCH = T::KCH, BNC = T::BNC, TM = T::TM, TN = T::TN,
                 KSTEPS = T::KSTEPS, NMFMA = T::NMFMA, LA = T::LA, LPT = T::LPT;
   static_assert(!T::IDLE_ROUNDS && !T::B_RAGGED_ROUNDS, "producer waves load whole rows per round");
-  static_assert(T::STAGED_F32_EPILOGUE, "f32 partials staged through LDS");
+  static_assert(T::STAGED_F32_EPILOGUE && !T::F32_HALF_BLOCKS,
+                "f32 partials staged through LDS in whole 32-row blocks");
   static_assert(KSTEPS == 4, "whole-k-tile fragment buffers sized for BK = 64");
   __shared__ u32x4 lds[STAGES * T::STAGE];
   auto stage_base = [&](int st) -> u32x4 * { return lds + st * T::STAGE; };

@@ -253,10 +253,12 @@
 // one wave of 192x64 (its 32x32x16 build spills)
 #define TBK_M16_TILES_192x64(X) X(192, 64, 64, 1, 1, 2)
 
-// 4 waves of 128x128 on 256x256 with 32-deep k-tiles in 3 or 4 LDS stages
-// (the same 128 KiB ring as the hand-scheduled 64-deep 2-stage tile, cut
-// into k-tiles of half the depth: half the loads and reads per barrier)
-#define TBK_M16_TILES_256x256(X) X(256, 256, 32, 2, 2, 3), X(256, 256, 32, 2, 2, 4)
+// 4 waves of 128x128 on 256x256 with 32-deep k-tiles: in 3 or 4 LDS stages
+// the same 128 KiB ring as the hand-scheduled 64-deep 2-stage tile, cut
+// into k-tiles of half the depth (half the loads and reads per barrier); in
+// 2 stages the key whose 32x32x16 build spills
+#define TBK_M16_TILES_256x256(X) \
+  X(256, 256, 32, 2, 2, 2), X(256, 256, 32, 2, 2, 3), X(256, 256, 32, 2, 2, 4)
 
 #define TBK_M16_TILES_192x128(X) \
   X(192, 128, 64, 2, 1, 2), X(192, 128, 64, 2, 1, 3), X(192, 128, 64, 2, 1, 4), \

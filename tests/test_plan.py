@@ -205,7 +205,8 @@ def test_mfma_instruction_choice():
     for kw in (dict(wide, M=520, N=200, exact=False), dict(wide, K=200, exact=False),
                dict(wide, c="f32"), dict(wide, c="f32", M=520, K=200, exact=False),
                dict(wide, bm=128, bn=128), dict(wide, bn=128, bk=32, stages=3),
-               dict(wide, bn=128, warps=2), dict(wide, bm=128, bn=128, warps=1)):
+               dict(wide, bn=128, warps=2), dict(wide, bm=128, bn=128, warps=1),
+               dict(wide, bk=32)):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_16X16X32, kw
     f32 = tb.plan_from_mlir(matmul_module(**dict(wide, c="f32")))
     assert f32.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out2_16x16x32"
@@ -215,8 +216,10 @@ def test_mfma_instruction_choice():
                     '"tb.reduction-mode" = "split_k_parallel"'), {}):
         assert launch(matmul_module(**kw)).config.mfma == tb.MFMA_32X32X16, kw
     # 32x32x16 builds of 128x128 wave tiles spill: refused at KernelConfig
-    # legality with the compiler's figures
-    for kw in (dict(wide, bk=32), dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"')):
+    # legality with the compiler's figures (4 waves on 256x256x32 take the
+    # 16x16x32 loop's build above; asked for 32x32x16 they are refused)
+    for kw in (dict(wide, bk=32, extra_op=', mma = "mfma_f32_32x32x16_f16"'),
+               dict(wide, extra_op=', mma = "mfma_f32_32x32x16_f16"')):
         with pytest.raises(tb.TbError, match=r"tb-build-program-mapping-plan: .* spills"):
             launch(matmul_module(**kw))
     text = tb_opt(matmul_module(**wide), f"--pass-pipeline={MAINLINE}").stdout

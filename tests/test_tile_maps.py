@@ -190,3 +190,93 @@ def test_plan_binds_every_feasible_tile():
                                 refused.append(((bm, bn, bk, nw, st), str(e)[:120]))
     assert not refused, refused
     assert bound >= 200
+
+
+# ---- the general loop's staged f32 epilogue (GemmTile F32_*, gemm_kernel) ----
+def f32_stage_params(bm, bn, bk, gm, gn, stages):
+    """GemmTile's f32 staging constants: row bytes, chunks per row, rows per
+    256-byte period, XOR width, rows per 64-lane read, rows per LDS pass."""
+    wtn = bn // gn
+    nw = gm * gn
+    rowb = wtn * 4
+    cpr = wtn // 4
+    rpp = 1 if rowb >= 256 else 256 // rowb
+    xor = min(cpr, 16)
+    rpi = 64 // cpr
+    ring = stages * (bm + bn) * bk * 2
+    br = 32 if nw * 32 * rowb <= ring else 16
+    assert nw * br * rowb <= ring, "no staging region fits the ring"
+    return rowb, cpr, rpp, xor, rpi, br
+
+
+def f32_stage_maps(wtn, rowb, cpr, rpp, xor, rpi, br, local_rows=True):
+    """Per pass h: {LDS byte address: (block row, logical 16-byte chunk)}
+    written by the active lanes, and [(lane, address, (block row, chunk))]
+    read back: restates the staged f32 epilogue of gemm_kernel."""
+    tn, hb = wtn // 32, 32 // br
+    nld = 32 // rpi
+    passes = []
+    for h in range(hb):
+        written, writers = {}, []
+        for lane in range(64):
+            rw, khalf = lane % 32, lane // 32
+            if rw // br != h:
+                continue
+            rl = rw % br if local_rows else rw
+            for j in range(tn):
+                for g in range(4):
+                    c = 8 * j + 2 * g + khalf
+                    addr = rl * rowb + (c ^ ((rl // rpp) % xor)) * 16
+                    assert addr not in written
+                    written[addr] = (rw, c)
+                    writers.append((lane, j, g, addr))
+        reads = []
+        for t in range(h * nld // hb, (h + 1) * nld // hb):
+            for lane in range(64):
+                r = (t - h * nld // hb) * rpi + lane // cpr
+                q = lane % cpr
+                addr = r * rowb + (q ^ ((r // rpp) % xor)) * 16
+                reads.append((lane, addr, (t * rpi + lane // cpr, q)))
+        passes.append((written, writers, reads))
+    return passes
+
+
+# (block, wave grid, stages, rows per pass): the reference's 128x64 case on
+# 4x1 waves takes 16-row passes (4 x 32 rows x 256 bytes > its 24 KiB ring),
+# as does 256x128x32 on 4x2 waves (64 KiB > 48 KiB); the others whole blocks
+F32_TILES = [((128, 64, 32), (4, 1), 2, 16), ((64, 128, 32), (1, 4), 2, 32),
+             ((64, 64, 32), (1, 1), 2, 32), ((64, 64, 32), (2, 2), 2, 32),
+             ((128, 128, 64), (2, 2), 2, 32), ((256, 128, 32), (4, 2), 2, 16),
+             ((128, 64, 64), (4, 2), 3, 32)]
+
+
+@pytest.mark.parametrize("tile", F32_TILES, ids=lambda t: f"{t[0]}_w{t[1]}_s{t[2]}_r{t[3]}")
+def test_f32_staged_epilogue_map(tile):
+    """Each pass writes its rows' chunks once, inside the region, and every
+    read finds the block row and chunk it stores; one 16-lane LDS cycle of a
+    write or a read touches 16 different 16-byte bank groups."""
+    (bm, bn, bk), (gm, gn), stages, rows = tile
+    rowb, cpr, rpp, xor, rpi, br = f32_stage_params(bm, bn, bk, gm, gn, stages)
+    assert br == rows
+    for written, writers, reads in f32_stage_maps(bn // gn, rowb, cpr, rpp, xor, rpi, br):
+        assert sorted(written) == list(range(0, br * rowb, 16)), "pass region not covered once"
+        for lane, addr, want in reads:
+            assert written[addr] == want, (lane, addr)
+        for j in range(bn // gn // 32):
+            for g in range(4):
+                addrs = [a for (l, jj, gg, a) in sorted(writers) if jj == j and gg == g]
+                for c0 in range(0, len(addrs), 16):
+                    assert _bank_conflict_ways(addrs[c0:c0 + 16], 16, 16) == 1
+        by_t = {}
+        for i, (lane, addr, _) in enumerate(reads):
+            by_t.setdefault(i // 64, []).append(addr)
+        for addrs in by_t.values():
+            assert _bank_conflict_ways(addrs, 16, 16) == 1
+
+
+def test_f32_staged_epilogue_half_needs_local_rows():
+    """Planted mistake: addressing a 16-row pass by the block row (rw) instead
+    of the row in the pass overruns the 16-row region."""
+    rowb, cpr, rpp, xor, rpi, br = f32_stage_params(128, 64, 32, 4, 1, 2)
+    written = f32_stage_maps(64, rowb, cpr, rpp, xor, rpi, br, local_rows=False)[1][0]
+    assert max(written) >= br * rowb
