@@ -12,10 +12,10 @@ Usage (under rocprofv3, the program after `--`):
 
 `--small-tiles` instead launches single-tile problems of the reference's
 small cases (64x64, 64x128 and 128x64 tiles on the wave counts its configs
-name, and the 64x64 tile on 4 waves beside its 1) as f16 C, plain f32 C and
-f32 C += A*B, `--reps` times each, back to back: a kernel trace of it shows
-what the output mode and the wave count cost at the size where a launch is
-all latency.
+name, the 64x64 tile on 4 waves beside its 1, and 128x128 on both MFMA
+shapes) as f16 C, plain f32 C and f32 C += A*B, `--reps` times each, back to
+back: a kernel trace of it shows what the output mode, the wave count and
+the MFMA shape cost at the size where a launch is all latency.
 """
 from __future__ import annotations
 
@@ -81,14 +81,17 @@ def main() -> int:
     return 0
 
 
-# (M, N, K, block_m, block_n, block_k, wave grid m, wave grid n): one tile each
-SMALL_TILES = [(64, 64, 32, 64, 64, 32, 1, 1), (64, 64, 32, 64, 64, 32, 2, 2),
-               (64, 64, 64, 64, 64, 32, 1, 1), (64, 64, 64, 64, 64, 64, 1, 1),
-               (128, 64, 32, 128, 64, 32, 4, 1), (64, 128, 32, 64, 128, 32, 1, 4)]
+# (M, N, K, block_m, block_n, block_k, wave grid m, wave grid n, MFMA
+# 16x16x32): one tile each
+SMALL_TILES = [(64, 64, 32, 64, 64, 32, 1, 1, False), (64, 64, 32, 64, 64, 32, 2, 2, False),
+               (64, 64, 64, 64, 64, 32, 1, 1, False), (64, 64, 64, 64, 64, 64, 1, 1, False),
+               (128, 64, 32, 128, 64, 32, 4, 1, False), (64, 128, 32, 64, 128, 32, 1, 4, False),
+               (128, 128, 32, 128, 128, 32, 2, 2, True), (128, 128, 32, 128, 128, 32, 2, 2, False),
+               (128, 128, 64, 128, 128, 64, 2, 2, True), (128, 128, 64, 128, 128, 64, 2, 2, False)]
 
 
 def small_tiles(tb, torch, dev, stream, reps) -> int:
-    for (M, N, K, bm, bn, bk, gm, gn) in SMALL_TILES:
+    for (M, N, K, bm, bn, bk, gm, gn, m16) in SMALL_TILES:
         A = torch.empty((M, K), dtype=torch.float16, device=dev)
         B = torch.empty((K, N), dtype=torch.float16, device=dev)
         tb.fill_seeded_f16(A, M, K, 0x5EED0A00 + K, 0, 1.0, stream=stream)
@@ -100,7 +103,8 @@ def small_tiles(tb, torch, dev, stream, reps) -> int:
                 acc_init=tb.ACC_INIT_LOAD_C if out == 2 else tb.ACC_INIT_ZERO,
                 block_m=bm, block_n=bn, block_k=bk, num_waves=gm * gn, wave_grid_m=gm,
                 wave_grid_n=gn, stages=2, mapping=tb.MAP_TILE, group_m=1, split_k=1,
-                reduction=tb.RED_NONE, num_programs=1, xcd_remap=0, mfma=tb.MFMA_32X32X16)
+                reduction=tb.RED_NONE, num_programs=1, xcd_remap=0,
+                mfma=tb.MFMA_16X16X32 if m16 else tb.MFMA_32X32X16)
             desc = tb.GemmDesc.from_config(cfg)
             C = torch.zeros((M, N), dtype=torch.float16 if out == 0 else torch.float32,
                             device=dev)
