@@ -112,6 +112,22 @@ def test_persistent_8192_192x128_tiles(device, persistent_8192_ref):
     _check_full(run_desc(desc, A, B, device), ref)
 
 
+def test_persistent_8192_f32_accumulate(device, persistent_8192_ref):
+    """8192^3 in the reference's semantics, f32 C += A*B, through the plan
+    (the 16x16x32 256x256x64 instance, 256 resident programs over 1024
+    tiles): each program adds four tiles' prior C inside their main loops
+    (128 k-tiles each) in turn. Every element against fp64 product + C."""
+    w = dataclasses.replace(configs.PERSISTENT, name="persistent_8192_f32", c_f32=True)
+    print(f"workload {w.name}", flush=True)
+    A, B, ref = persistent_8192_ref
+    desc = tb.plan_from_mlir(w.mlir())
+    assert desc.kernel_name == "tb_gemm_gfx950_256x256x64_w2x2_s2_out2_16x16x32"
+    assert desc.config.num_programs == 256
+    init = np.random.default_rng(8192).uniform(-1, 1, (w.M, w.N)).astype(np.float32)
+    got = run_desc(desc, A, B, device, c_init=init)
+    _check_full(got, ref + init)
+
+
 # The configurations of the reference's examples/*.mlir and contract tests
 # (f32 C, 1-4 warps), which the plan maps to C += A B, the reference's
 # tb.matmul semantics: C starts from a seeded non-zero value and the oracle
