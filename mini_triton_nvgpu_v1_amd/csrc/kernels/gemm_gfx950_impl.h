@@ -1481,58 +1481,58 @@ __global__ __launch_bounds__(WGM *WGN * 64, 1) void gemm_kernel(GemmParams p) {
         }
 #pragma unroll
         for (int h = 0; h < HB; ++h) {
-        // accumulators in: lane l holds row l % 32, columns 32j + 8g + 4(l / 32);
-        // in pass h only the lanes of rows h BR .. h BR + BR - 1 (row rw % BR
-        // of the pass region). The lanes read what other lanes wrote, which
-        // the compiler's one-thread memory model does not see: a lane that
-        // skipped this pass's writes would reuse its previous pass's read of
-        // the same address (measured: the reads moved into the masked write
-        // block). The memory clobbers make every lane read after the writes
-        // (LDS executes one wave's operations in order; no instruction).
-        asm volatile("" ::: "memory");
-        if (HB == 1 || rw / BR == h) {
-          const int rl = rw % BR;
+          // accumulators in: lane l holds row l % 32, columns 32j + 8g + 4(l / 32);
+          // in pass h only the lanes of rows h BR .. h BR + BR - 1 (row rw % BR
+          // of the pass region). The lanes read what other lanes wrote, which
+          // the compiler's one-thread memory model does not see: a lane that
+          // skipped this pass's writes would reuse its previous pass's read of
+          // the same address (measured: the reads moved into the masked write
+          // block). The memory clobbers make every lane read after the writes
+          // (LDS executes one wave's operations in order; no instruction).
+          asm volatile("" ::: "memory");
+          if (HB == 1 || rw / BR == h) {
+            const int rl = rw % BR;
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int cs = (8 * j + 2 * g + khalf) ^ ((rl / T::F32_RPP) % T::F32_XOR);
-              *(TBK_LDS f32x4 *)(wl + rl * T::F32_ROWB + cs * 16) =
-                  (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
-                          acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+              for (int g = 0; g < 4; ++g) {
+                const int cs = (8 * j + 2 * g + khalf) ^ ((rl / T::F32_RPP) % T::F32_XOR);
+                *(TBK_LDS f32x4 *)(wl + rl * T::F32_ROWB + cs * 16) =
+                    (f32x4){acc[i][j][4 * g + 0], acc[i][j][4 * g + 1],
+                            acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+              }
+          }
+          asm volatile("" ::: "memory");
+          // whole row segments out: segment t of the block is row t F32_RPI +
+          // l / F32_CPR, in pass t / NLDH
+#pragma unroll
+          for (int t = h * NLDH; t < (h + 1) * NLDH; ++t) {
+            const int r = (t - h * NLDH) * T::F32_RPI + lane / T::F32_CPR; // row in the pass
+            const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
+            f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
+            if constexpr (OUT == kOutF32Accum) {
+              v += old[t];
+              if constexpr (EPI) {
+                const epi_f32x4 b = epi_load_bias(ea, col, p.N);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  v[e] = epi_apply1(v[e], b[e], ea);
+              }
             }
-        }
-        asm volatile("" ::: "memory");
-        // whole row segments out: segment t of the block is row t F32_RPI +
-        // l / F32_CPR, in pass t / NLDH
-#pragma unroll
-        for (int t = h * NLDH; t < (h + 1) * NLDH; ++t) {
-          const int r = (t - h * NLDH) * T::F32_RPI + lane / T::F32_CPR; // row in the pass
-          const int cs = q ^ ((r / T::F32_RPP) % T::F32_XOR);
-          f32x4 v = *(const TBK_LDS f32x4 *)(wl + r * T::F32_ROWB + cs * 16);
-          if constexpr (OUT == kOutF32Accum) {
-            v += old[t];
-            if constexpr (EPI) {
-              const epi_f32x4 b = epi_load_bias(ea, col, p.N);
+            if constexpr (OUT == kOutF32Atomic) {
+              // past the edges off[t] is kOob: the atomics are dropped
 #pragma unroll
               for (int e = 0; e < 4; ++e)
-                v[e] = epi_apply1(v[e], b[e], ea);
+                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v[e], rc, off[t] + 4u * e, 0, 0);
+            } else {
+              // f32 results (split-K partials, plain f32 C) are written once
+              // and not read again by this kernel: non-temporal, which leaves
+              // less dirty data in L2 for the kernel-end release (split-K 512^2
+              // x 16384: 15.7 -> 15.1 us per GEMM); C += A*B keeps the default
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
+                                                     0, OUT == kOutF32Partial ? kStoreNT : 0);
             }
           }
-          if constexpr (OUT == kOutF32Atomic) {
-            // past the edges off[t] is kOob: the atomics are dropped
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v[e], rc, off[t] + 4u * e, 0, 0);
-          } else {
-            // f32 results (split-K partials, plain f32 C) are written once
-            // and not read again by this kernel: non-temporal, which leaves
-            // less dirty data in L2 for the kernel-end release (split-K 512^2
-            // x 16384: 15.7 -> 15.1 us per GEMM); C += A*B keeps the default
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off[t],
-                                                   0, OUT == kOutF32Partial ? kStoreNT : 0);
-          }
-        }
         }
       }
     } else if constexpr (OUT == kOutF32Partial || OUT == kOutF32Accum) {
