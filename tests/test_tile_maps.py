@@ -1,5 +1,7 @@
 """CPU checks of the general loop's LDS maps for the 192-wide and 8-wave
-tiles, and of the plan's tile coverage.
+tiles and for its staged f32 epilogue (whole 32-row blocks, or 16-row
+halves where a block does not fit the ring), and of the plan's tile
+coverage.
 
 The kernel (csrc/kernels/gemm_gfx950_impl.h, GemmTile / gemm_kernel) fills
 each operand's LDS stage in rounds of one 16-byte chunk per lane: round i of
