@@ -288,3 +288,22 @@ def test_descriptors_and_errors_from_many_threads():
     for t in threads:
         t.join()
     assert not failures, "\n".join(failures[:10])
+
+
+def test_small_tile_profile_problems_bind():
+    """Every single-tile problem of `profiling --small-tiles` (the command of
+    the committed small-tile kernel trace) binds its instance in each output
+    mode, on the MFMA shape it names."""
+    from mini_triton_nvgpu_v1_amd import profiling
+    for (M, N, K, bm, bn, bk, gm, gn, m16) in profiling.SMALL_TILES:
+        for out in (0, 1, 2):
+            d = tb.GemmDesc.from_config(tb.GemmConfig(
+                m=M, n=N, k=K, lda=K, ldb=N, ldc=N,
+                c_dtype=tb.DTYPE_F16 if out == 0 else tb.DTYPE_F32,
+                acc_init=tb.ACC_INIT_LOAD_C if out == 2 else tb.ACC_INIT_ZERO,
+                block_m=bm, block_n=bn, block_k=bk, num_waves=gm * gn, wave_grid_m=gm,
+                wave_grid_n=gn, stages=2, mapping=tb.MAP_TILE, group_m=1, split_k=1,
+                reduction=tb.RED_NONE, num_programs=1, xcd_remap=0,
+                mfma=tb.MFMA_16X16X32 if m16 else tb.MFMA_32X32X16))
+            assert d.kernel_name.endswith(f"_out{out}" + ("_16x16x32" if m16 else "")), \
+                d.kernel_name
